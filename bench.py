@@ -1,0 +1,199 @@
+"""Benchmark of the FP8 paged-KV hot path on one MI355X.
+
+Workload (the Qwen3-8B layer decode): 32 q heads, 8 kv heads, head_dim 128,
+block 256, batch 64, every sequence at context 4096, a 2048-block FP8 pool
+filled by store_fp8_kvcache from bf16 N(0,1) K/V, block tables drawn from a
+seeded permutation, bf16 N(0,1) queries.  One step is one decode-attention
+pass over the batch; consecutive steps alternate between two disjoint halves
+of the pool (each a valid draw of the workload), so the 1.1 GB footprint
+keeps the 256 MB MALL from serving the reads.
+
+Printed JSON: ``value`` is decode-attention HBM GB/s on algorithmic bytes
+(2112 B per context token for H_kv 8 -- fp8 K+V rows and their fp32 scales --
+plus queries, outputs, tables and lengths), ``roofline`` compares the decode
+op (split-KV kernel + combine) with the 8 TB/s HBM peak, ``store`` reports
+store_kvcache tokens/s on the 262,144-token pool fill, and ``cpu_baseline``
+times the oracle's torch-CPU decode on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+HQ, HK, D, BS = 32, 8, 128, 256
+BATCH, CTX, POOL = 64, 4096, 2048
+
+
+def decode_bytes(batch, ctx, hq, hk, d, act_bytes=2):
+    """Algorithmic bytes of one decode pass: each K/V byte and scale once per
+    kv head, the query and output once, the table entries and lengths."""
+    kv = batch * ctx * (2 * hk * d + 2 * hk * 4)
+    qo = batch * hq * d * act_bytes * 2
+    tables = 4 * (batch * ((ctx + BS - 1) // BS) + batch)
+    return kv + qo + tables
+
+
+def store_bytes(n, hk, d, act_bytes=2, slot_bytes=8):
+    return n * (2 * hk * d * act_bytes + 2 * hk * d + 2 * hk * 4 + slot_bytes)
+
+
+def build_workload(dev):
+    from microserve_amd import store_fp8_kvcache
+    gen = torch.Generator().manual_seed(2024)
+    perm = torch.randperm(POOL, generator=gen).to(torch.int32)
+    pages = CTX // BS
+    tables = [perm[:BATCH * pages].view(BATCH, pages).contiguous(),
+              perm[BATCH * pages:2 * BATCH * pages].view(BATCH, pages).contiguous()]
+    kc = torch.zeros(POOL, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(POOL, BS, HK, device=dev)
+    vs = torch.ones_like(ks)
+    pos = torch.arange(CTX)
+    fills = []
+    for t in tables:
+        slots = (t[:, pos // BS].long() * BS + pos % BS).reshape(-1)
+        key = torch.randn(slots.numel(), HK, D, generator=gen).bfloat16()
+        value = torch.randn(slots.numel(), HK, D, generator=gen).bfloat16()
+        fills.append((key.to(dev), value.to(dev), slots.to(dev)))
+        store_fp8_kvcache(fills[-1][0], fills[-1][1], kc, vc, ks, vs, fills[-1][2])
+    query = torch.randn(BATCH, HQ, D, generator=gen).bfloat16().to(dev)
+    seqlens = torch.full((BATCH,), CTX, dtype=torch.int32, device=dev)
+    return dict(kc=kc, vc=vc, ks=ks, vs=vs, query=query, seqlens=seqlens,
+                tables=[t.to(dev) for t in tables], fills=fills)
+
+
+def time_store_fill(w, iters=5):
+    from microserve_amd import store_fp8_kvcache
+    key, value, slots = w["fills"][0]
+    n = slots.numel()
+    stream = torch.cuda.current_stream()
+    store_fp8_kvcache(key, value, w["kc"], w["vc"], w["ks"], w["vs"], slots)
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    times = []
+    for i in range(iters):
+        key, value, slots = w["fills"][i % 2]
+        start.record(stream)
+        store_fp8_kvcache(key, value, w["kc"], w["vc"], w["ks"], w["vs"], slots)
+        end.record(stream)
+        end.synchronize()
+        times.append(start.elapsed_time(end) * 1e-3)
+    t = sorted(times)[len(times) // 2]
+    return {"tokens": n, "tokens_per_s": n / t, "us": t * 1e6,
+            "gbs": store_bytes(n, HK, D) / t / 1e9,
+            "frac": store_bytes(n, HK, D) / t / 1e9 / HBM_PEAK_GBS}
+
+
+def cpu_baseline(w, budget_s=15.0):
+    """Oracle torch-CPU decode on a bounded sample of the same workload:
+    whole sequences of the batch until about budget_s of CPU work."""
+    import numpy as np
+    from oracle import fp8_oracle as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    kc = w["kc"].view(torch.uint8).cpu()
+    vc = w["vc"].view(torch.uint8).cpu()
+    ks, vs = w["ks"].cpu(), w["vs"].cpu()
+    q = w["query"].cpu()
+    tables = w["tables"][0].cpu()
+    lens = np.full(BATCH, CTX)
+    done, t_total = 0, 0.0
+    while done < BATCH and t_total < budget_s:
+        t0 = time.perf_counter()
+        O.decode_attention(q[done:done + 1], kc, vc, ks, vs, lens[done:done + 1],
+                           tables[done:done + 1], D ** -0.5)
+        t_total += time.perf_counter() - t0
+        done += 1
+    gbs = decode_bytes(done, CTX, HQ, HK, D) / t_total / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{done} of {BATCH} sequences (4096 tokens each) of the "
+                      f"Qwen3-8B decode batch, torch fp32 oracle, {t_total:.1f} s"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build runs the path on a single "
+              "MI355X (multi-GPU sharding is design-only)", file=sys.stderr)
+        sys.exit(2)
+    from microserve_amd import decode_num_splits, fp8_decode_attention
+    dev = "cuda:0"
+    w = build_workload(dev)
+    torch.cuda.synchronize()
+    out = torch.empty_like(w["query"])
+    scale = D ** -0.5
+
+    def step(i):
+        fp8_decode_attention(w["query"], w["kc"], w["vc"], w["ks"], w["vs"],
+                             w["seqlens"], w["tables"][i % 2], scale, out=out)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        evs[i][0].record(stream)
+        step(i)
+        evs[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_launch = sorted(a.elapsed_time(b) * 1e-3 for a, b in evs)
+    avg_launch = sum(per_launch) / len(per_launch)
+    nbytes = decode_bytes(BATCH, CTX, HQ, HK, D)
+    ms_per_step = wall / args.steps * 1e3
+    value = nbytes / (wall / args.steps) / 1e9
+    achieved = nbytes / avg_launch / 1e9
+    store = time_store_fill(w)
+    result = {
+        "metric": "FP8 paged decode-attn HBM GB/s (% of peak) + store_kvcache tokens/s, Qwen3-8B",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp8-e4m3 KV, bf16 q/out, fp32 softmax",
+        "data": "synthetic: seeded N(0,1) bf16 K/V/q quantized by store_fp8_kvcache",
+        "config": {"workload": "Qwen3-8B layer decode: 32 q / 8 kv heads, head_dim 128, "
+                               "block 256, batch 64 x context 4096, 2048-block fp8 pool",
+                   "splits": decode_num_splits(BATCH, HQ, HK, CTX // BS, BS),
+                   "algorithmic_bytes_per_step": nbytes},
+        "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "roofline": {"bound": "hbm", "kernel": "decode_fp8_kernel + decode_combine_kernel",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "avg_launch_us": round(avg_launch * 1e6, 2),
+                     "median_launch_us": round(per_launch[len(per_launch) // 2] * 1e6, 2),
+                     "traffic": None},
+        "store": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in store.items()},
+    }
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(w)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

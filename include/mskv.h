@@ -1,0 +1,143 @@
+/*
+ * mskv -- C ABI of the MI355X (gfx950) FP8 paged-KV library.
+ *
+ * Plain pointers and sizes only: every tensor argument is a device pointer to
+ * contiguous memory, every stream argument is a hipStream_t passed as void*.
+ * Launches are asynchronous on that stream; no entry point allocates device
+ * memory, synchronizes, or reads device memory on the host, so all of them
+ * may be captured into a HIP graph.
+ *
+ * Cache layout (the reference runner's, microserve/engine/model_runner.py:76-83):
+ *   k_cache, v_cache           uint8 (OCP FP8 e4m3fn) [num_blocks, block_size, num_kv_heads, head_dim]
+ *   k_scale_cache, v_scale_cache  float32             [num_blocks, block_size, num_kv_heads]
+ * Cache row r = block * block_size + offset holds token slot r.
+ *
+ * Return value: 0 on success, a negative MSKV_E* code for rejected arguments,
+ * or a positive hipError_t from the launch.  mskv_status_string() names it.
+ */
+#ifndef MSKV_H
+#define MSKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* activation element types (query, key, value, output) */
+#define MSKV_FLOAT16 0
+#define MSKV_BFLOAT16 1
+/* slot_mapping element types */
+#define MSKV_INT32 0
+#define MSKV_INT64 1
+
+#define MSKV_OK 0
+#define MSKV_EINVAL (-1)       /* null pointer, bad size or inconsistent shape */
+#define MSKV_EUNSUPPORTED (-2) /* valid shape the kernels do not implement     */
+#define MSKV_EWORKSPACE (-3)   /* workspace missing or smaller than required   */
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int mskv_version(void);
+
+/* Human-readable text for a status code returned by any entry point. */
+const char* mskv_status_string(int status);
+
+/*
+ * Quantize K/V rows to FP8 e4m3fn with one fp32 scale per (token, kv head)
+ * and scatter them through slot_mapping.
+ *
+ * Replaces store_fp8_kvcache, microserve/layers/fp8_kv_cache.py:42-61
+ * (kernel :11-39): scale = max(amax_d |x|, 1e-8) / 448, byte =
+ * e4m3fn(clamp(x / scale, -448, 448)) with IEEE fp32 division, written at
+ * cache row slot_mapping[t].  key/value: [num_tokens, num_kv_heads, head_dim]
+ * in act_dtype.  Slots outside [0, num_slots) are skipped (num_slots =
+ * num_blocks * block_size); the reference never produces them.
+ * Supported: head_dim == 128.
+ */
+int mskv_store_fp8_kvcache(const void* key, const void* value,
+                           void* k_cache, void* v_cache,
+                           float* k_scale_cache, float* v_scale_cache,
+                           const void* slot_mapping, int slot_dtype,
+                           int64_t num_tokens, int num_kv_heads, int head_dim,
+                           int64_t num_slots, int act_dtype, void* stream);
+
+/*
+ * Number of split-KV partitions mskv_fp8_decode_attention uses for a shape.
+ * Depends on shapes only (never on device sequence lengths), so a captured
+ * graph stays valid for any lengths up to max_blocks_per_seq * block_size.
+ */
+int mskv_decode_num_splits(int batch, int num_q_heads, int num_kv_heads,
+                           int max_blocks_per_seq, int block_size);
+
+/* Workspace bytes mskv_fp8_decode_attention needs for num_splits (0 if 1). */
+size_t mskv_decode_workspace_bytes(int batch, int num_q_heads, int head_dim,
+                                   int num_splits);
+
+/*
+ * Paged decode attention over the FP8 cache: one query token per sequence.
+ *
+ * Replaces fp8_decode_attention, microserve/layers/fp8_decode_attention.py:62-101
+ * (kernel :8-59): q head h reads kv head h / (num_q_heads / num_kv_heads);
+ * token p of sequence b is cache row block_tables[b][p / block_size] *
+ * block_size + p % block_size for p < cache_seqlens[b]; scores are
+ * q . (k * k_scale) * softmax_scale; out = softmax(scores) @ (v * v_scale),
+ * or zeros when cache_seqlens[b] == 0.
+ * query/out: [batch, num_q_heads, head_dim] in act_dtype; cache_seqlens:
+ * int32 [batch]; block_tables: int32 [batch, max_blocks_per_seq], -1 padded.
+ * Block ids outside [0, num_blocks) read as empty.  num_splits must be the
+ * value mskv_decode_num_splits returns for the shape; when it is above 1 the
+ * workspace must hold mskv_decode_workspace_bytes bytes.
+ * Supported: head_dim == 128, block_size % 32 == 0, and a GQA group
+ * (num_q_heads / num_kv_heads) of at most 16 or a multiple of 16.
+ */
+int mskv_fp8_decode_attention(const void* query, const void* k_cache,
+                              const void* v_cache, const float* k_scale_cache,
+                              const float* v_scale_cache,
+                              const int32_t* cache_seqlens,
+                              const int32_t* block_tables, void* out,
+                              int batch, int num_q_heads, int num_kv_heads,
+                              int head_dim, int block_size, int64_t num_blocks,
+                              int max_blocks_per_seq, float softmax_scale,
+                              int act_dtype, int num_splits, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/*
+ * Causal paged prefill over the FP8 cache for a varlen batch whose new
+ * tokens are already stored in the cache.
+ *
+ * Replaces fp8_chunk_prefill_attention,
+ * microserve/layers/fp8_chunk_prefill_attention.py:70-109 (kernel :8-67),
+ * generalized from one sequence (block_table.view(-1), scalar prefix_len) to
+ * the varlen batch the runner describes with cu_seqlens_q / cu_seqlens_k
+ * (microserve/engine/model_runner.py:184-192).  Sequence s owns query rows
+ * [cu_seqlens_q[s], cu_seqlens_q[s+1]) and context length
+ * Lk = cu_seqlens_k[s+1] - cu_seqlens_k[s]; query i sees cache positions
+ * p < (Lk - Lq) + i + 1 (fp8_chunk_prefill_attention.py:52-54).
+ * When cu_seqlens_q and cu_seqlens_k are both NULL the batch is one
+ * sequence of total_q queries over prefix_len + total_q positions, exactly
+ * the reference's signature.  QK^T and PV run as FP8 MFMA contractions with
+ * a per-row fp32 scale on the query and on the probabilities.
+ * query/out: [total_q, num_q_heads, head_dim] in act_dtype; block_tables:
+ * int32 [num_seqs, max_blocks_per_seq].
+ * Supported: head_dim == 128, block_size % 128 == 0, GQA group <= 16 or a
+ * multiple of 16.
+ */
+int mskv_fp8_prefill_attention(const void* query, const void* k_cache,
+                               const void* v_cache, const float* k_scale_cache,
+                               const float* v_scale_cache,
+                               const int32_t* block_tables,
+                               const int32_t* cu_seqlens_q,
+                               const int32_t* cu_seqlens_k, int prefix_len,
+                               void* out, int num_seqs, int64_t total_q,
+                               int max_seqlen_q, int num_q_heads,
+                               int num_kv_heads, int head_dim, int block_size,
+                               int64_t num_blocks, int max_blocks_per_seq,
+                               float softmax_scale, int act_dtype,
+                               void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSKV_H */

@@ -1,0 +1,70 @@
+"""Paged attention layer (drop-in for the FP8 branch of
+``microserve/layers/attention.py``).
+
+The runner injects ``k_cache``/``v_cache`` (fp8 ``[NB+1, BS, H_kv, D]``
+views), ``k_scale_cache``/``v_scale_cache`` (fp32 ``[NB+1, BS, H_kv]``) and
+``kv_cache_dtype`` as plain attributes (``model_runner.py:111-122``).
+``forward`` stores the step's K/V first and then attends, dispatching on the
+global ``Context``'s mode (``attention.py:36-61``).
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from microserve_amd.context import AttentionMode, get_context
+from microserve_amd.fp8_chunk_prefill_attention import (
+    fp8_chunk_prefill_attention,
+    fp8_varlen_prefill_attention,
+)
+from microserve_amd.fp8_decode_attention import fp8_decode_attention
+from microserve_amd.fp8_kv_cache import store_fp8_kvcache
+
+
+class Attention(nn.Module):
+    """Paged attention over an injected FP8 KV cache."""
+
+    def __init__(self, num_heads: int, head_dim: int, scale: float,
+                 num_kv_heads: int):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads
+        self.k_cache = self.v_cache = torch.tensor([])
+        self.k_scale_cache = self.v_scale_cache = None
+        self.kv_cache_dtype = "fp8_e4m3"
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        ctx = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        assert k_cache.numel(), "k_cache was not injected: allocate the KV cache first"
+        if self.kv_cache_dtype != "fp8_e4m3":
+            # The fp16-cache branch (attention.py:63-85) runs on flash-attn
+            # and is outside this library.
+            raise NotImplementedError(
+                f"kv_cache_dtype {self.kv_cache_dtype!r}: only the fp8_e4m3 path is provided")
+        store_fp8_kvcache(k, v, k_cache, v_cache, self.k_scale_cache,
+                          self.v_scale_cache, ctx.slot_mapping)
+        if ctx.mode is AttentionMode.DECODE:
+            return fp8_decode_attention(
+                q, k_cache, v_cache, self.k_scale_cache, self.v_scale_cache,
+                ctx.cache_seqlens, ctx.block_tables, self.scale)
+        if ctx.mode is AttentionMode.PREFILL:
+            # The reference runs flash_attn_varlen_func on the unquantized
+            # q/k/v here (attention.py:49-55).  This library attends over the
+            # just-stored FP8 cache instead, which needs the block tables.
+            if ctx.block_tables is None:
+                raise NotImplementedError(
+                    "fresh PREFILL needs ctx.block_tables: attention runs over "
+                    "the stored FP8 cache")
+            return fp8_varlen_prefill_attention(
+                q, k_cache, v_cache, self.k_scale_cache, self.v_scale_cache,
+                ctx.block_tables, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
+                ctx.max_seqlen_q, self.scale)
+        if ctx.mode is AttentionMode.CHUNK_PREFILL:
+            return fp8_chunk_prefill_attention(
+                q, k_cache, v_cache, self.k_scale_cache, self.v_scale_cache,
+                ctx.block_tables, ctx.prefix_len, self.scale)
+        raise RuntimeError(f"unsupported attention mode: {ctx.mode}")

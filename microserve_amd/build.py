@@ -1,0 +1,66 @@
+"""Build recipe for the mskv HIP library (gfx950 only).
+
+Compiles every source under ``csrc/`` with hipcc into
+``microserve_amd/libmskv.so``.  Run ``python -m microserve_amd.build``.
+The library is built in-tree so it travels with the repository snapshot.
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "libmskv.so")
+ARCH = "gfx950"
+
+# -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32.
+# No fast-math: the store path relies on hipcc's correctly rounded fp32
+# division and on IEEE fp32 denormals.
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def sources():
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC)
+                  if f.endswith((".hip", ".cpp")))
+
+
+def build(verbose: bool = False) -> str:
+    hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    objs = []
+    tmp = os.path.join(HERE, "_build")
+    os.makedirs(tmp, exist_ok=True)
+    for src in sources():
+        obj = os.path.join(tmp, os.path.basename(src) + ".o")
+        cmd = [hipcc, *HIP_FLAGS, "-c", src, "-o", obj]
+        if src.endswith(".cpp"):
+            cmd = [hipcc, "-O2", "-std=c++17", "-fPIC", "-Wall", "-c", src, "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        # hipcc's host pass warns that it does not know packed-fp32-ops
+        err = "\n".join(x for x in r.stderr.splitlines()
+                        if "packed-fp32-ops" not in x and x.strip())
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc failed on {src}:\n{err}")
+        if err and verbose:
+            print(err, file=sys.stderr)
+        objs.append(obj)
+    tmp_out = OUT + ".tmp"
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp_out]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stderr}")
+    os.replace(tmp_out, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

@@ -1,0 +1,383 @@
+// Paged decode attention over the FP8 e4m3fn cache, split-KV + LSE combine.
+//
+// Semantics follow microserve/layers/fp8_decode_attention.py:16-58: q head h
+// reads kv head h / group; token p of sequence b is cache row
+// block_tables[b][p / BS] * BS + p % BS; score = (q . k8) * k_scale *
+// softmax_scale; out = sum softmax * v8 * v_scale; zeros when seq_len == 0.
+//
+// MI355X design (one wave per (sequence, kv head, split)):
+//  * K/V are read once per kv head: the whole GQA group of q heads (up to
+//    16) rides in the N dimension of the MFMAs.
+//  * QK^T runs as S^T = K . Q^T on v_mfma_f32_16x16x32_{bf16,f16}: K rows
+//    come straight from HBM as 16-byte buffer loads (lane (g, i) holds token
+//    i, bytes [16g,16g+16) and [64+16g,64+16g+16)) and are converted to the
+//    query's 16-bit type exactly (e4m3 is a subset of fp16 and bf16); Q uses
+//    the same d permutation, so the contraction is the plain dot product.
+//  * The S^T accumulator leaves lane (g, n) holding tokens {4g+r, 16+4g+r}
+//    of head n -- exactly the B-operand layout of O^T = V^T . P^T, so the
+//    probabilities never move between lanes.  P is scaled by the per-token
+//    v_scale and rounded to bf16 (fp32 range) for the PV MFMA.
+//  * V^T's A operand needs eight tokens per lane at one d: V goes row-major
+//    into a per-wave LDS tile and comes back transposed with
+//    ds_read_b64_tr_b8, then is converted fp8 -> bf16 in registers.
+//  * Online softmax in base 2 (v_exp_f32); the row max is a two-step xor
+//    reduction across the four lane groups that share a head.
+//  * Split-KV: the host picks pages-per-split from shapes only; each split
+//    writes (o / l, m + log2 l) partials and decode_combine_kernel merges
+//    them.  With one split the kernel writes the output directly.
+//  * Every page is read through a buffer resource sized to that page; an
+//    invalid block id gives a zero-length resource (loads return 0) and its
+//    tokens are masked, so a bad table entry cannot fault.
+#include <math.h>
+
+#include "mskv_device.h"
+#include "../../include/mskv.h"
+
+namespace mskv {
+
+constexpr int kStep = 32;          // tokens per inner step (one LDS V tile)
+constexpr int kMaxPagesPerSplit = 4;
+constexpr int kTargetWaves = 4096;
+
+struct DecodeArgs {
+  const uint16_t* q;
+  const uint8_t* kc;
+  const uint8_t* vc;
+  const float* ks;
+  const float* vs;
+  const int32_t* seqlens;
+  const int32_t* bt;
+  uint16_t* out;
+  float* part_o;
+  float* part_lse;
+  int hq, hk, group, qgroups, bs, w, splits, pages_per_split;
+  int64_t num_blocks;
+  float scale_log2;
+};
+
+struct StepLoads {
+  u32x4 k0a, k0b, k1a, k1b;  // K rows: tile 0 (tokens 0..15), tile 1 (16..31)
+  u32x4 v[4];                // V rows 8c + lane/8, 16-byte column lane%8
+  float kscale, vscale;      // scales of token lane & 31
+  int valid;                 // tokens of this step below the sequence end
+};
+
+__device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
+                                          int t0, int t_end, int lane,
+                                          StepLoads& s) {
+  const int page = t0 / a.bs;
+  const int off = t0 - page * a.bs;
+  const int blk = a.bt[(int64_t)b * a.w + page];
+  const bool ok = blk >= 0 && (int64_t)blk < a.num_blocks;
+  const int64_t bo = ok ? blk : 0;
+  const uint32_t page_bytes = (uint32_t)a.bs * a.hk * kHeadDim;
+  const uint32_t spage_bytes = (uint32_t)a.bs * a.hk * 4u;
+  const auto kr = make_rsrc(a.kc + bo * page_bytes, ok ? page_bytes : 0u);
+  const auto vr = make_rsrc(a.vc + bo * page_bytes, ok ? page_bytes : 0u);
+  const auto ksr = make_rsrc(a.ks + bo * a.bs * a.hk, ok ? spage_bytes : 0u);
+  const auto vsr = make_rsrc(a.vs + bo * a.bs * a.hk, ok ? spage_bytes : 0u);
+  const uint32_t rstride = (uint32_t)a.hk * kHeadDim;
+  const uint32_t base = (uint32_t)off * rstride + (uint32_t)kvh * kHeadDim;
+  const int g = lane >> 4, n = lane & 15;
+  const uint32_t kt0 = base + (uint32_t)n * rstride + 16u * g;
+  const uint32_t kt1 = kt0 + 16u * rstride;
+  s.k0a = buf_load16(kr, kt0);
+  s.k0b = buf_load16(kr, kt0 + 64u);
+  s.k1a = buf_load16(kr, kt1);
+  s.k1b = buf_load16(kr, kt1 + 64u);
+  const uint32_t vb = base + (uint32_t)(lane >> 3) * rstride + 16u * (lane & 7);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) s.v[c] = buf_load16(vr, vb + 8u * c * rstride);
+  const uint32_t so = (((uint32_t)off + (lane & 31)) * a.hk + kvh) * 4u;
+  s.kscale = buf_load_f32(ksr, so);
+  s.vscale = buf_load_f32(vsr, so);
+  s.valid = ok ? min(kStep, t_end - t0) : 0;
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void decode_fp8_kernel(DecodeArgs a) {
+  using A = Act<T>;
+  using x8 = typename A::x8;
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds[kStep * kHeadDim];
+  __shared__ __attribute__((aligned(16))) float s_lds[2 * kStep];
+
+  const int lane = threadIdx.x;
+  const int g = lane >> 4, n = lane & 15;
+  const int unit = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
+  const int kvh = unit / a.qgroups;
+  const int hig = (unit - kvh * a.qgroups) * 16 + n;  // head within its group
+  const bool head_ok = hig < a.group;
+  const int qh = kvh * a.group + hig;
+  // tokens past the block table's width are not addressable: ignore them
+  const int L = min(a.seqlens[b], a.w * a.bs);
+  const int split_tokens = a.pages_per_split * a.bs;
+  const int t_begin = split * split_tokens;
+
+  if (L <= 0) {
+    if (a.splits == 1 && split == 0 && head_ok) {
+      uint16_t* op = a.out + ((int64_t)b * a.hq + qh) * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{0u, 0u};
+    }
+    return;
+  }
+  if (t_begin >= L) return;
+  const int t_end = min(L, t_begin + split_tokens);
+
+  // Q^T as the B operand: lane (g, n) holds head n at d in
+  // [16g, 16g+16) and [64+16g, 64+16g+16), eight per MFMA k-step.
+  x8 qop[4];
+  if (head_ok) {
+    const u32x4* qp =
+        reinterpret_cast<const u32x4*>(a.q + ((int64_t)b * a.hq + qh) * kHeadDim);
+    qop[0] = __builtin_bit_cast(x8, qp[2 * g]);
+    qop[1] = __builtin_bit_cast(x8, qp[2 * g + 1]);
+    qop[2] = __builtin_bit_cast(x8, qp[8 + 2 * g]);
+    qop[3] = __builtin_bit_cast(x8, qp[9 + 2 * g]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) qop[j] = __builtin_bit_cast(x8, u32x4{0u, 0u, 0u, 0u});
+  }
+
+  f32x4 acc[8];
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = -INFINITY, l = 0.0f;
+
+  // ds_read_b64_tr_b8: in each 16-lane group, result byte e of lane i comes
+  // from the address supplied by lane 2e + i/8, plus i%8.  Lane i therefore
+  // supplies token slot e = i/2 at column half i%2.
+  const int i16 = lane & 15;
+  const int slot = i16 >> 1;
+  const int trow = slot < 4 ? 4 * g + slot : 16 + 4 * g + (slot - 4);
+  const uint32_t tr_base = (uint32_t)trow * kHeadDim + 8u * (i16 & 1);
+
+  StepLoads cur, nxt;
+  load_step(a, b, kvh, t_begin, t_end, lane, cur);
+  for (int t0 = t_begin; t0 < t_end; t0 += kStep) {
+    // stage V (rows past the sequence end are zeroed: their P is 0, and a
+    // stray NaN byte would otherwise poison the MFMA sum) and the scales
+    const int valid = cur.valid;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int row = 8 * c + (lane >> 3);
+      const u32x4 v = row < valid ? cur.v[c] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(v_lds + row * kHeadDim + 16 * (lane & 7)) = v;
+    }
+    s_lds[lane] = lane < 32 ? cur.kscale : cur.vscale;
+    __syncthreads();
+    if (t0 + kStep < t_end) load_step(a, b, kvh, t0 + kStep, t_end, lane, nxt);
+
+    // S^T = K . Q^T for tokens [0,16) and [16,32) of the step
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+    x8 ka;
+    A::fp8x4_to(cur.k0a[0], ka, 0); A::fp8x4_to(cur.k0a[1], ka, 4); s0 = A::mfma(ka, qop[0], s0);
+    A::fp8x4_to(cur.k0a[2], ka, 0); A::fp8x4_to(cur.k0a[3], ka, 4); s0 = A::mfma(ka, qop[1], s0);
+    A::fp8x4_to(cur.k0b[0], ka, 0); A::fp8x4_to(cur.k0b[1], ka, 4); s0 = A::mfma(ka, qop[2], s0);
+    A::fp8x4_to(cur.k0b[2], ka, 0); A::fp8x4_to(cur.k0b[3], ka, 4); s0 = A::mfma(ka, qop[3], s0);
+    A::fp8x4_to(cur.k1a[0], ka, 0); A::fp8x4_to(cur.k1a[1], ka, 4); s1 = A::mfma(ka, qop[0], s1);
+    A::fp8x4_to(cur.k1a[2], ka, 0); A::fp8x4_to(cur.k1a[3], ka, 4); s1 = A::mfma(ka, qop[1], s1);
+    A::fp8x4_to(cur.k1b[0], ka, 0); A::fp8x4_to(cur.k1b[1], ka, 4); s1 = A::mfma(ka, qop[2], s1);
+    A::fp8x4_to(cur.k1b[2], ka, 0); A::fp8x4_to(cur.k1b[3], ka, 4); s1 = A::mfma(ka, qop[3], s1);
+
+    const f32x4 ksc0 = *reinterpret_cast<const f32x4*>(s_lds + 4 * g);
+    const f32x4 ksc1 = *reinterpret_cast<const f32x4*>(s_lds + 16 + 4 * g);
+    const f32x4 vsc0 = *reinterpret_cast<const f32x4*>(s_lds + 32 + 4 * g);
+    const f32x4 vsc1 = *reinterpret_cast<const f32x4*>(s_lds + 48 + 4 * g);
+    float x[8];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      x[r] = (4 * g + r < valid) ? s0[r] * ksc0[r] * a.scale_log2 : -INFINITY;
+      x[4 + r] = (16 + 4 * g + r < valid) ? s1[r] * ksc1[r] * a.scale_log2 : -INFINITY;
+    }
+    float tmax = x[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, x[e]);
+    tmax = wave_max_xor(tmax, 16);
+    tmax = wave_max_xor(tmax, 32);
+    const float m_new = fmaxf(m, tmax);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float alpha = exp2_fast(m - m_use);
+    float psum = 0.0f;
+    bf16x8 pt;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = exp2_fast(x[e] - m_use);
+      psum += p;
+      const float vsc = e < 4 ? vsc0[e] : vsc1[e - 4];
+      pt[e] = (__bf16)(x[e] == -INFINITY ? 0.0f : p * vsc);
+    }
+    l = l * alpha + psum;
+    m = m_new;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+
+    // O^T += V^T . P^T, one 16-wide d tile per MFMA
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const i32x2 raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+          reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
+              (__attribute__((address_space(3))) uint8_t*)v_lds + tr_base + 16 * dt));
+      const bf16x8 vt = fp8x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pt, acc[dt], 0, 0, 0);
+    }
+    __syncthreads();
+    cur = nxt;
+  }
+
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (!head_ok) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  if (a.splits == 1) {
+    uint16_t* op = a.out + ((int64_t)b * a.hq + qh) * kHeadDim;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const f32x4 o = acc[dt] * inv;
+      const uint32_t lo = (uint32_t)A::from_f32(o[0]) | ((uint32_t)A::from_f32(o[1]) << 16);
+      const uint32_t hi = (uint32_t)A::from_f32(o[2]) | ((uint32_t)A::from_f32(o[3]) << 16);
+      *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{lo, hi};
+    }
+  } else {
+    const int64_t row = ((int64_t)b * a.hq + qh) * a.splits + split;
+    float* po = a.part_o + row * kHeadDim;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt)
+      *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * g) = acc[dt] * inv;
+    if (g == 0) a.part_lse[row] = l > 0.0f ? m + __log2f(l) : -INFINITY;
+  }
+}
+
+// out[b, h, :] = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M) over the
+// splits that hold tokens of sequence b; zeros when there are none.
+template <typename T>
+__global__ __launch_bounds__(64) void decode_combine_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_lse,
+    const int32_t* __restrict__ seqlens, uint16_t* __restrict__ out, int hq,
+    int splits, int split_tokens, int max_tokens) {
+  const int row = blockIdx.x;  // b * hq + h
+  const int b = row / hq;
+  const int lane = threadIdx.x;
+  const int L = min(seqlens[b], max_tokens);
+  const int nvalid = L <= 0 ? 0 : min(splits, (L + split_tokens - 1) / split_tokens);
+  const float* lse = part_lse + (int64_t)row * splits;
+  float M = -INFINITY;
+  for (int s = 0; s < nvalid; ++s) M = fmaxf(M, lse[s]);
+  float o0 = 0.0f, o1 = 0.0f, den = 0.0f;
+  if (M != -INFINITY) {
+    const float* po = part_o + (int64_t)row * splits * kHeadDim + 2 * lane;
+    for (int s = 0; s < nvalid; ++s) {
+      const float w = exp2_fast(lse[s] - M);
+      const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kHeadDim);
+      o0 += w * v.x;
+      o1 += w * v.y;
+      den += w;
+    }
+  }
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  const uint32_t pk = (uint32_t)Act<T>::from_f32(o0 * inv) |
+                      ((uint32_t)Act<T>::from_f32(o1 * inv) << 16);
+  *reinterpret_cast<uint32_t*>(out + (int64_t)row * kHeadDim + 2 * lane) = pk;
+}
+
+static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
+
+template <typename T>
+static hipError_t launch_decode(const DecodeArgs& a, int batch,
+                                hipStream_t stream) {
+  const dim3 grid((unsigned)(a.hk * a.qgroups), (unsigned)a.splits, (unsigned)batch);
+  hipLaunchKernelGGL(decode_fp8_kernel<T>, grid, dim3(64), 0, stream, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || a.splits == 1) return e;
+  hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)(batch * a.hq)),
+                     dim3(64), 0, stream, a.part_o, a.part_lse, a.seqlens,
+                     a.out, a.hq, a.splits, a.pages_per_split * a.bs, a.w * a.bs);
+  return hipGetLastError();
+}
+
+static int pages_per_split_of(int splits, int w) {
+  return splits <= 1 ? w : (w + splits - 1) / splits;
+}
+
+}  // namespace mskv
+
+extern "C" int mskv_decode_num_splits(int batch, int num_q_heads,
+                                      int num_kv_heads, int max_blocks_per_seq,
+                                      int block_size) {
+  (void)block_size;
+  if (batch <= 0 || num_kv_heads <= 0 || num_q_heads <= 0 ||
+      max_blocks_per_seq <= 0)
+    return 1;
+  const int group = num_q_heads / num_kv_heads;
+  const int64_t base = (int64_t)batch * num_kv_heads * mskv::qgroups_of(group);
+  const int w = max_blocks_per_seq;
+  int64_t pps = (w * base + mskv::kTargetWaves - 1) / mskv::kTargetWaves;
+  if (pps < 1) pps = 1;
+  if (pps > mskv::kMaxPagesPerSplit) pps = mskv::kMaxPagesPerSplit;
+  const int64_t splits = (w + pps - 1) / pps;
+  return (int)splits;
+}
+
+extern "C" size_t mskv_decode_workspace_bytes(int batch, int num_q_heads,
+                                              int head_dim, int num_splits) {
+  if (num_splits <= 1 || batch <= 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
+  return (size_t)batch * num_q_heads * num_splits * (head_dim + 1) * sizeof(float);
+}
+
+extern "C" int mskv_fp8_decode_attention(
+    const void* query, const void* k_cache, const void* v_cache,
+    const float* k_scale_cache, const float* v_scale_cache,
+    const int32_t* cache_seqlens, const int32_t* block_tables, void* out,
+    int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+    int64_t num_blocks, int max_blocks_per_seq, float softmax_scale,
+    int act_dtype, int num_splits, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
+      num_blocks < 0 || max_blocks_per_seq <= 0 || num_splits <= 0)
+    return MSKV_EINVAL;
+  if (act_dtype != MSKV_FLOAT16 && act_dtype != MSKV_BFLOAT16) return MSKV_EINVAL;
+  if (num_q_heads % num_kv_heads != 0) return MSKV_EINVAL;
+  const int group = num_q_heads / num_kv_heads;
+  if (head_dim != mskv::kHeadDim || block_size % mskv::kStep != 0 ||
+      (group > 16 && group % 16 != 0))
+    return MSKV_EUNSUPPORTED;
+  // page offsets are 32-bit buffer offsets
+  if ((int64_t)block_size * num_kv_heads * head_dim > 0x7FFFFFFFLL) return MSKV_EUNSUPPORTED;
+  if (num_splits != mskv_decode_num_splits(batch, num_q_heads, num_kv_heads,
+                                           max_blocks_per_seq, block_size))
+    return MSKV_EINVAL;
+  if (batch == 0) return MSKV_OK;
+  if (!query || !k_cache || !v_cache || !k_scale_cache || !v_scale_cache ||
+      !cache_seqlens || !block_tables || !out)
+    return MSKV_EINVAL;
+  const size_t need = mskv_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+  if (need > 0 && (!workspace || workspace_bytes < need)) return MSKV_EWORKSPACE;
+
+  mskv::DecodeArgs a;
+  a.q = (const uint16_t*)query;
+  a.kc = (const uint8_t*)k_cache;
+  a.vc = (const uint8_t*)v_cache;
+  a.ks = k_scale_cache;
+  a.vs = v_scale_cache;
+  a.seqlens = cache_seqlens;
+  a.bt = block_tables;
+  a.out = (uint16_t*)out;
+  a.part_o = (float*)workspace;
+  a.part_lse = need > 0 ? (float*)workspace + (size_t)batch * num_q_heads * num_splits * head_dim
+                        : nullptr;
+  a.hq = num_q_heads;
+  a.hk = num_kv_heads;
+  a.group = group;
+  a.qgroups = mskv::qgroups_of(group);
+  a.bs = block_size;
+  a.w = max_blocks_per_seq;
+  a.splits = num_splits;
+  a.pages_per_split = mskv::pages_per_split_of(num_splits, max_blocks_per_seq);
+  a.num_blocks = num_blocks;
+  a.scale_log2 = softmax_scale * mskv::kLog2e;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = act_dtype == MSKV_BFLOAT16 ? mskv::launch_decode<__bf16>(a, batch, s)
+                                            : mskv::launch_decode<_Float16>(a, batch, s);
+  return (int)e;
+}

@@ -1,0 +1,123 @@
+// Device helpers shared by the mskv kernels (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mskv {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
+
+constexpr int kHeadDim = 128;
+constexpr float kFp8Max = 448.0f;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- buffers --
+// Raw buffer resources: loads past num_records return zeros instead of
+// faulting, so a page whose block id is invalid is read through a
+// zero-length resource.  Word 3 is the gfx9 data-format word.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* p,
+                                                            uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0,
+                                           (int)bytes, 0x00020000);
+}
+
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r,
+                                            uint32_t off) {
+  return __builtin_bit_cast(u32x4,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r,
+                                              uint32_t off) {
+  return __builtin_bit_cast(float,
+                            __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+
+// ------------------------------------------------------- activation types --
+// Two instantiations of one code path: fp16 and bf16 activations.
+template <typename T>
+struct Act;
+
+template <>
+struct Act<_Float16> {
+  static constexpr int kId = 0;
+  using x8 = f16x8;
+  __device__ static float to_f32(uint16_t bits) {
+    return (float)__builtin_bit_cast(_Float16, bits);
+  }
+  __device__ static uint16_t from_f32(float x) {
+    return __builtin_bit_cast(uint16_t, (_Float16)x);
+  }
+  // four e4m3fn bytes -> four exact fp16 values (e4m3 is a subset of fp16)
+  __device__ static void fp8x4_to(uint32_t w, x8& dst, int at) {
+    f16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
+    f16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, true);
+    dst[at + 0] = lo[0];
+    dst[at + 1] = lo[1];
+    dst[at + 2] = hi[0];
+    dst[at + 3] = hi[1];
+  }
+  __device__ static f32x4 mfma(const x8& a, const x8& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Act<__bf16> {
+  static constexpr int kId = 1;
+  using x8 = bf16x8;
+  __device__ static float to_f32(uint16_t bits) {
+    return __builtin_bit_cast(float, (uint32_t)bits << 16);
+  }
+  __device__ static uint16_t from_f32(float x) {
+    return __builtin_bit_cast(uint16_t, (__bf16)x);
+  }
+  // four e4m3fn bytes -> four exact bf16 values (e4m3 is a subset of bf16)
+  __device__ static void fp8x4_to(uint32_t w, x8& dst, int at) {
+    bf16x2 lo = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, false);
+    bf16x2 hi = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, true);
+    dst[at + 0] = lo[0];
+    dst[at + 1] = lo[1];
+    dst[at + 2] = hi[0];
+    dst[at + 3] = hi[1];
+  }
+  __device__ static f32x4 mfma(const x8& a, const x8& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+// eight e4m3fn bytes (two dwords) -> eight exact bf16 values
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
+  bf16x8 r;
+  Act<__bf16>::fp8x4_to(w0, r, 0);
+  Act<__bf16>::fp8x4_to(w1, r, 4);
+  return r;
+}
+
+// Four fp32 values -> four e4m3fn bytes (RNE, sign kept on zero).  The inputs
+// must already lie in [-448, 448].
+__device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c,
+                                               float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+__device__ __forceinline__ float exp2_fast(float x) {
+  return __builtin_amdgcn_exp2f(x);
+}
+
+__device__ __forceinline__ float wave_max_xor(float v, int mask) {
+  return fmaxf(v, __shfl_xor(v, mask));
+}
+
+}  // namespace mskv

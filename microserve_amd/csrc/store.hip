@@ -1,0 +1,145 @@
+// store_kvcache for the FP8 paged cache: quantize K/V rows to e4m3fn with a
+// per-(token, kv head) fp32 scale and scatter them through slot_mapping.
+//
+// Follows microserve/layers/fp8_kv_cache.py:11-39 (kernel) and :42-61
+// (wrapper).  Layout of the work: eight lanes own one (token, kv head) pair
+// and each lane holds 16 of its 128 elements of K and of V, so a lane issues
+// two 16-byte loads per tensor and one 16-byte store per tensor; the row
+// amax is an 8-lane xor reduction.  The division x / scale is the IEEE fp32
+// division (hipcc's default correctly rounded sequence), and the e4m3fn
+// conversion is the hardware RNE convert on the clamped value, which matches
+// torch's CPU cast bit for bit (sign kept on zero, subnormals kept).
+#include "mskv_device.h"
+#include "../../include/mskv.h"
+
+namespace mskv {
+
+constexpr int kStoreLanesPerRow = kHeadDim / 16;  // 8
+constexpr int kStoreThreads = 256;
+constexpr int kStoreRowsPerBlock = kStoreThreads / kStoreLanesPerRow;
+
+template <typename T>
+__device__ __forceinline__ void unpack16(const u32x4& a, const u32x4& b,
+                                         float* x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = Act<T>::to_f32((uint16_t)(a[i] & 0xFFFFu));
+    x[2 * i + 1] = Act<T>::to_f32((uint16_t)(a[i] >> 16));
+    x[8 + 2 * i] = Act<T>::to_f32((uint16_t)(b[i] & 0xFFFFu));
+    x[8 + 2 * i + 1] = Act<T>::to_f32((uint16_t)(b[i] >> 16));
+  }
+}
+
+// Row amax over 8 lanes, scale, quantized bytes of this lane's 16 elements.
+__device__ __forceinline__ float quantize16(const float* x, u32x4& q) {
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(x[i]));
+  amax = wave_max_xor(amax, 1);
+  amax = wave_max_xor(amax, 2);
+  amax = wave_max_xor(amax, 4);
+  const float scale = fmaxf(amax, 1e-8f) / kFp8Max;
+  float y[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i)
+    y[i] = fminf(fmaxf(x[i] / scale, -kFp8Max), kFp8Max);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    q[i] = pack_fp8x4(y[4 * i], y[4 * i + 1], y[4 * i + 2], y[4 * i + 3]);
+  return scale;
+}
+
+template <typename T, typename SlotT>
+__global__ __launch_bounds__(kStoreThreads) void store_fp8_kernel(
+    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
+    uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
+    float* __restrict__ k_scale, float* __restrict__ v_scale,
+    const SlotT* __restrict__ slots, int64_t rows, int num_kv_heads,
+    int64_t num_slots) {
+  const int sub = threadIdx.x % kStoreLanesPerRow;
+  const int64_t row =
+      (int64_t)blockIdx.x * kStoreRowsPerBlock + threadIdx.x / kStoreLanesPerRow;
+  if (row >= rows) return;  // whole 8-lane groups leave together
+  const int64_t tok = row / num_kv_heads;
+  const int head = (int)(row - tok * num_kv_heads);
+  const int64_t slot = (int64_t)slots[tok];
+
+  const u32x4* kp = reinterpret_cast<const u32x4*>(key + row * kHeadDim + sub * 16);
+  const u32x4* vp = reinterpret_cast<const u32x4*>(value + row * kHeadDim + sub * 16);
+  const u32x4 k0 = __builtin_nontemporal_load(kp);
+  const u32x4 k1 = __builtin_nontemporal_load(kp + 1);
+  const u32x4 v0 = __builtin_nontemporal_load(vp);
+  const u32x4 v1 = __builtin_nontemporal_load(vp + 1);
+
+  float x[16];
+  u32x4 kq, vq;
+  unpack16<T>(k0, k1, x);
+  const float ks = quantize16(x, kq);
+  unpack16<T>(v0, v1, x);
+  const float vs = quantize16(x, vq);
+
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t dst = slot * num_kv_heads + head;
+  *reinterpret_cast<u32x4*>(k_cache + dst * kHeadDim + sub * 16) = kq;
+  *reinterpret_cast<u32x4*>(v_cache + dst * kHeadDim + sub * 16) = vq;
+  if (sub == 0) {
+    k_scale[dst] = ks;
+    v_scale[dst] = vs;
+  }
+}
+
+template <typename T>
+static hipError_t launch_store(const void* key, const void* value, void* kc,
+                               void* vc, float* ks, float* vs,
+                               const void* slots, int slot_dtype,
+                               int64_t num_tokens, int hk, int64_t num_slots,
+                               hipStream_t stream) {
+  const int64_t rows = num_tokens * hk;
+  const int64_t blocks = (rows + kStoreRowsPerBlock - 1) / kStoreRowsPerBlock;
+  if (slot_dtype == MSKV_INT64)
+    hipLaunchKernelGGL((store_fp8_kernel<T, int64_t>), dim3((unsigned)blocks),
+                       dim3(kStoreThreads), 0, stream, (const uint16_t*)key,
+                       (const uint16_t*)value, (uint8_t*)kc, (uint8_t*)vc, ks,
+                       vs, (const int64_t*)slots, rows, hk, num_slots);
+  else
+    hipLaunchKernelGGL((store_fp8_kernel<T, int32_t>), dim3((unsigned)blocks),
+                       dim3(kStoreThreads), 0, stream, (const uint16_t*)key,
+                       (const uint16_t*)value, (uint8_t*)kc, (uint8_t*)vc, ks,
+                       vs, (const int32_t*)slots, rows, hk, num_slots);
+  return hipGetLastError();
+}
+
+}  // namespace mskv
+
+extern "C" int mskv_store_fp8_kvcache(const void* key, const void* value,
+                                      void* k_cache, void* v_cache,
+                                      float* k_scale_cache,
+                                      float* v_scale_cache,
+                                      const void* slot_mapping, int slot_dtype,
+                                      int64_t num_tokens, int num_kv_heads,
+                                      int head_dim, int64_t num_slots,
+                                      int act_dtype, void* stream) {
+  if (num_tokens < 0 || num_kv_heads <= 0 || num_slots < 0) return MSKV_EINVAL;
+  if (slot_dtype != MSKV_INT32 && slot_dtype != MSKV_INT64) return MSKV_EINVAL;
+  if (act_dtype != MSKV_FLOAT16 && act_dtype != MSKV_BFLOAT16) return MSKV_EINVAL;
+  if (head_dim != mskv::kHeadDim) return MSKV_EUNSUPPORTED;
+  if (num_tokens == 0) return MSKV_OK;
+  if (!key || !value || !k_cache || !v_cache || !k_scale_cache ||
+      !v_scale_cache || !slot_mapping)
+    return MSKV_EINVAL;
+  if ((num_tokens * num_kv_heads + mskv::kStoreRowsPerBlock - 1) /
+          mskv::kStoreRowsPerBlock > 0x7FFFFFFFLL)
+    return MSKV_EUNSUPPORTED;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e =
+      act_dtype == MSKV_BFLOAT16
+          ? mskv::launch_store<__bf16>(key, value, k_cache, v_cache,
+                                       k_scale_cache, v_scale_cache,
+                                       slot_mapping, slot_dtype, num_tokens,
+                                       num_kv_heads, num_slots, s)
+          : mskv::launch_store<_Float16>(key, value, k_cache, v_cache,
+                                         k_scale_cache, v_scale_cache,
+                                         slot_mapping, slot_dtype, num_tokens,
+                                         num_kv_heads, num_slots, s);
+  return (int)e;
+}

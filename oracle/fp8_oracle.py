@@ -202,17 +202,17 @@ def decode_attention(query, k_cache, v_cache, k_scale_cache, v_scale_cache,
     b, hq, d = q.shape
     hk = k_cache.shape[2]
     group = hq // hk
-    head_map = torch.arange(hq) // group
     lens = [int(x) for x in _as_t(cache_seqlens).reshape(-1).tolist()]
     tables = _as_t(block_tables, torch.int64)
     out = torch.zeros(b, hq, d, dtype=torch.float32)
     for i, n in enumerate(lens):
         if n <= 0:
             continue
-        k = dequant_gather(k_cache, k_scale_cache, tables[i], n)[:, head_map]
-        v = dequant_gather(v_cache, v_scale_cache, tables[i], n)[:, head_map]
-        scores = torch.einsum("hd,lhd->hl", q[i], k) * softmax_scale
-        out[i] = torch.einsum("hl,lhd->hd", scores.softmax(-1), v)
+        k = dequant_gather(k_cache, k_scale_cache, tables[i], n)   # [L, H_kv, D]
+        v = dequant_gather(v_cache, v_scale_cache, tables[i], n)
+        qg = q[i].view(hk, group, d)            # q head h -> kv head h // group
+        scores = torch.einsum("kgd,lkd->kgl", qg, k) * softmax_scale
+        out[i] = torch.einsum("kgl,lkd->kgd", scores.softmax(-1), v).reshape(hq, d)
     return out
 
 
@@ -271,7 +271,7 @@ def varlen_prefill_attention(query, k_cache, v_cache, k_scale_cache,
     q = _as_t(query).float()
     tq, hq, d = q.shape
     hk = k_cache.shape[2]
-    head_map = torch.arange(hq) // (hq // hk)
+    group = hq // hk
     cu_q = [int(x) for x in _as_t(cu_seqlens_q).reshape(-1).tolist()]
     cu_k = [int(x) for x in _as_t(cu_seqlens_k).reshape(-1).tolist()]
     tables = _as_t(block_tables, torch.int64)
@@ -282,15 +282,15 @@ def varlen_prefill_attention(query, k_cache, v_cache, k_scale_cache,
         if lq <= 0:
             continue
         prefix = lk - lq
-        k = dequant_gather(k_cache, k_scale_cache, tables[s], lk)[:, head_map]
-        v = dequant_gather(v_cache, v_scale_cache, tables[s], lk)[:, head_map]
-        qs = q[cu_q[s]:cu_q[s + 1]]                                # [Lq, H, D]
-        scores = torch.einsum("ihd,lhd->hil", qs, k) * softmax_scale
+        k = dequant_gather(k_cache, k_scale_cache, tables[s], lk)   # [Lk, H_kv, D]
+        v = dequant_gather(v_cache, v_scale_cache, tables[s], lk)
+        qs = q[cu_q[s]:cu_q[s + 1]].view(lq, hk, group, d)
+        scores = torch.einsum("ikgd,lkd->kgil", qs, k) * softmax_scale
         pos = torch.arange(lk)[None, :]
         visible = (prefix + torch.arange(lq) + 1)[:, None]
-        scores = scores.masked_fill(~(pos < visible)[None], float("-inf"))
-        out[cu_q[s]:cu_q[s + 1]] = torch.einsum(
-            "hil,lhd->ihd", scores.softmax(-1), v)
+        scores = scores.masked_fill(~(pos < visible)[None, None], float("-inf"))
+        o = torch.einsum("kgil,lkd->ikgd", scores.softmax(-1), v)
+        out[cu_q[s]:cu_q[s + 1]] = o.reshape(lq, hq, d)
     return out
 
 

@@ -1,0 +1,105 @@
+"""The drop-in ``Attention`` layer + ``Context`` on the GPU: store-then-attend
+in each mode (``attention.py:36-61``) against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8_oracle as O
+from tests import gpu_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+from microserve_amd import (  # noqa: E402
+    Attention, AttentionMode, Context, reset_context, set_context)
+
+
+def _layer(hq=32, hk=8, nb=16):
+    attn = Attention(hq, H.D, H.D ** -0.5, hk)
+    attn.k_cache, attn.v_cache, attn.k_scale_cache, attn.v_scale_cache = H.alloc_cache(nb, H.BLOCK, hk)
+    attn.kv_cache_dtype = "fp8_e4m3"
+    return attn
+
+
+def _np_caches(attn):
+    return H.cache_to_numpy(attn.k_cache, attn.v_cache, attn.k_scale_cache, attn.v_scale_cache)
+
+
+def test_attention_chunk_then_decode():
+    gen = torch.Generator().manual_seed(301)
+    attn = _layer()
+    table = torch.tensor([[5, 2, 9]], dtype=torch.int32)
+    # chunk prefill: 300 tokens already cached, 40 new
+    pre_k = H.randn(gen, (300, 8, H.D), torch.bfloat16)
+    pre_v = H.randn(gen, (300, 8, H.D), torch.bfloat16)
+    pos = torch.arange(300)
+    slots = table[0, pos // H.BLOCK].long() * H.BLOCK + pos % H.BLOCK
+    from microserve_amd import store_fp8_kvcache
+    store_fp8_kvcache(pre_k.to(H.DEV), pre_v.to(H.DEV), attn.k_cache, attn.v_cache,
+                      attn.k_scale_cache, attn.v_scale_cache, slots.to(H.DEV))
+    q = H.randn(gen, (40, 32, H.D), torch.bfloat16)
+    k = H.randn(gen, (40, 8, H.D), torch.bfloat16)
+    v = H.randn(gen, (40, 8, H.D), torch.bfloat16)
+    pos = torch.arange(300, 340)
+    slots = table[0, pos // H.BLOCK].long() * H.BLOCK + pos % H.BLOCK
+    set_context(Context(mode=AttentionMode.CHUNK_PREFILL, slot_mapping=slots.to(H.DEV),
+                        block_tables=table.to(H.DEV), prefix_len=300, query_len=40,
+                        cache_seqlens=torch.tensor([340], dtype=torch.int32, device=H.DEV)))
+    try:
+        out = attn(q.to(H.DEV), k.to(H.DEV), v.to(H.DEV))
+    finally:
+        reset_context()
+    kc, vc, ks, vs = _np_caches(attn)
+    ref = O.chunk_prefill_attention(q, kc, vc, ks, vs, table[0], 300, H.D ** -0.5)
+    H.assert_attention_close(out, ref)
+    # the chunk's own K/V were stored bit-exactly at their slots
+    kq, _ = O.quantize_rows(k.float().numpy())
+    assert np.array_equal(kc.reshape(-1, 8, H.D)[slots.numpy()], kq)
+    # one decode step at position 340
+    q = H.randn(gen, (1, 32, H.D), torch.bfloat16)
+    k = H.randn(gen, (1, 8, H.D), torch.bfloat16)
+    v = H.randn(gen, (1, 8, H.D), torch.bfloat16)
+    slot = torch.tensor([int(table[0, 340 // H.BLOCK]) * H.BLOCK + 340 % H.BLOCK])
+    set_context(Context(mode=AttentionMode.DECODE, slot_mapping=slot.to(H.DEV),
+                        cache_seqlens=torch.tensor([341], dtype=torch.int32, device=H.DEV),
+                        block_tables=table.to(H.DEV)))
+    try:
+        out = attn(q.to(H.DEV), k.to(H.DEV), v.to(H.DEV))
+    finally:
+        reset_context()
+    kc, vc, ks, vs = _np_caches(attn)
+    ref = O.decode_attention(q, kc, vc, ks, vs, np.array([341]), table, H.D ** -0.5)
+    H.assert_attention_close(out, ref)
+
+
+def test_attention_fresh_prefill_over_stored_cache():
+    gen = torch.Generator().manual_seed(311)
+    attn = _layer(nb=8)
+    lens = [100, 37]
+    tables, slots = H.paged_layout(gen, lens, 8)
+    q = H.randn(gen, (137, 32, H.D), torch.bfloat16)
+    k = H.randn(gen, (137, 8, H.D), torch.bfloat16)
+    v = H.randn(gen, (137, 8, H.D), torch.bfloat16)
+    cu = torch.tensor([0, 100, 137], dtype=torch.int32)
+    set_context(Context(mode=AttentionMode.PREFILL, cu_seqlens_q=cu.to(H.DEV),
+                        cu_seqlens_k=cu.to(H.DEV), max_seqlen_q=100, max_seqlen_k=100,
+                        slot_mapping=slots.to(H.DEV), block_tables=tables.to(H.DEV)))
+    try:
+        out = attn(q.to(H.DEV), k.to(H.DEV), v.to(H.DEV))
+    finally:
+        reset_context()
+    kc, vc, ks, vs = _np_caches(attn)
+    ref = O.varlen_prefill_attention(q, kc, vc, ks, vs, tables, cu, cu, H.D ** -0.5)
+    H.assert_attention_close(out, ref)
+
+
+def test_attention_unknown_mode_raises():
+    attn = _layer(nb=2)
+    set_context(Context(mode="bogus", slot_mapping=torch.zeros(1, dtype=torch.int64, device=H.DEV)))
+    try:
+        with pytest.raises(RuntimeError):
+            attn(torch.zeros(1, 32, H.D, dtype=torch.bfloat16, device=H.DEV),
+                 torch.zeros(1, 8, H.D, dtype=torch.bfloat16, device=H.DEV),
+                 torch.zeros(1, 8, H.D, dtype=torch.bfloat16, device=H.DEV))
+    finally:
+        reset_context()

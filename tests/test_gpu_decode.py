@@ -1,0 +1,240 @@
+"""GPU parity of fp8_decode_attention against the oracle
+(``fp8_decode_attention.py:16-58``): outputs within 2e-2 max-abs and
+1e-2 relative (Frobenius) error, plus size-independent properties at the
+Qwen3-8B / 32B shapes."""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8_oracle as O
+from tests import gpu_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+sys.path.insert(0, GOLDEN)
+import cases  # noqa: E402
+
+from microserve_amd import (  # noqa: E402
+    decode_num_splits, fp8_decode_attention, store_fp8_kvcache)
+
+
+def _setup(seed, lens, hq, hk, num_blocks, dtype=torch.bfloat16, kscale=1.0,
+           vscale=1.0, qscale=1.0, block_size=H.BLOCK):
+    gen = torch.Generator().manual_seed(seed)
+    tables, slots = H.paged_layout(gen, lens, num_blocks, block_size)
+    n = slots.numel()
+    key = H.randn(gen, (n, hk, H.D), dtype, kscale)
+    value = H.randn(gen, (n, hk, H.D), dtype, vscale)
+    query = H.randn(gen, (len(lens), hq, H.D), dtype, qscale)
+    caches = H.alloc_cache(num_blocks, block_size, hk)
+    if n:
+        store_fp8_kvcache(key.to(H.DEV), value.to(H.DEV), *caches, slots.to(H.DEV))
+    return query, tables, caches
+
+
+def _run_and_check(query, lens, tables, caches, atol=2e-2, rtol=1e-2):
+    scale = H.D ** -0.5
+    seqlens = torch.tensor(lens, dtype=torch.int32)
+    out = fp8_decode_attention(query.to(H.DEV), *caches, seqlens.to(H.DEV),
+                               tables.to(H.DEV), scale)
+    torch.cuda.synchronize()
+    kc, vc, ks, vs = H.cache_to_numpy(*caches)
+    ref = O.decode_attention(query, kc, vc, ks, vs, seqlens, tables, scale)
+    return H.assert_attention_close(out, ref, atol, rtol), out
+
+
+def test_decode_reference_case():
+    """tests/test_fp8_kv_attention.py::test_decode's shape and tolerance."""
+    g = np.load(os.path.join(GOLDEN, "ref_shapes.npz"))
+    c = cases.decode_case()
+    caches = H.alloc_cache(c["num_blocks"])
+    store_fp8_kvcache(c["key"].to(H.DEV), c["value"].to(H.DEV), *caches, c["slots"].to(H.DEV))
+    out = fp8_decode_attention(c["query"].to(H.DEV), *caches,
+                               torch.tensor(c["lengths"], dtype=torch.int32, device=H.DEV),
+                               c["tables"].to(H.DEV), cases.D ** -0.5)
+    err = (out.float().cpu() - torch.from_numpy(g["dec_out"]).half().float()).abs().max().item()
+    assert torch.isfinite(out).all()
+    assert err < 0.004, err
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_qwen3_06b_config(dtype):
+    """Qwen3-0.6B layer: 16 q / 8 kv heads, batch 4, lengths U[1, 1024], a
+    randomly permuted 64-block pool."""
+    gen = torch.Generator().manual_seed(31)
+    lens = torch.randint(1, 1025, (4,), generator=gen).tolist()
+    query, tables, caches = _setup(32, lens, 16, 8, 64, dtype)
+    _run_and_check(query, lens, tables, caches)
+
+
+@pytest.mark.parametrize("hq,hk", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1), (32, 2), (64, 2)])
+def test_decode_gqa_groups(hq, hk):
+    lens = [1, 255, 256, 257, 700, 0, 1023, 33]
+    query, tables, caches = _setup(41 + hq + hk, lens, hq, hk, 40)
+    _run_and_check(query, lens, tables, caches)
+
+
+def test_decode_zero_length_and_padded_rows():
+    """Runner padding (``model_runner.py:268-273``): rows with seq_len 0 and an
+    all -1 table give zeros; real rows are unaffected."""
+    lens = [300, 0, 5, 0]
+    query, tables, caches = _setup(51, lens, 32, 8, 8)
+    (_, _), out = _run_and_check(query, lens, tables, caches)
+    assert (out[1] == 0).all() and (out[3] == 0).all()
+
+
+def test_decode_no_split_path():
+    """A batch large enough that the kernel writes the output directly."""
+    lens = [int(x) for x in torch.randint(1, 512, (512,), generator=torch.Generator().manual_seed(5))]
+    assert decode_num_splits(512, 32, 8, 2, H.BLOCK) == 1
+    query, tables, caches = _setup(61, lens, 32, 8, 1100)
+    _run_and_check(query, lens, tables, caches)
+
+
+def test_decode_invalid_block_ids_read_as_empty():
+    """Block ids outside the pool are skipped instead of read (an extension:
+    the reference never produces them)."""
+    lens = [512, 512]
+    query, tables, caches = _setup(71, lens, 32, 8, 4)
+    bad = tables.clone()
+    bad[0, 1] = 1 << 20          # second page of sequence 0 is out of the pool
+    out = fp8_decode_attention(query.to(H.DEV), *caches,
+                               torch.tensor(lens, dtype=torch.int32, device=H.DEV),
+                               bad.to(H.DEV), H.D ** -0.5)
+    kc, vc, ks, vs = H.cache_to_numpy(*caches)
+    ref0 = O.decode_attention(query[:1], kc, vc, ks, vs, torch.tensor([256]), tables[:1], H.D ** -0.5)
+    ref1 = O.decode_attention(query[1:], kc, vc, ks, vs, torch.tensor([512]), tables[1:], H.D ** -0.5)
+    H.assert_attention_close(out[:1], ref0)
+    H.assert_attention_close(out[1:], ref1)
+
+
+def test_decode_qwen3_8b_full_shape():
+    """Batch 64 x 4096 tokens, 32 q / 8 kv heads, 2048-block permuted pool."""
+    lens = [4096] * 64
+    query, tables, caches = _setup(81, lens, 32, 8, 2048)
+    _run_and_check(query, lens, tables, caches)
+
+
+def test_decode_block_relabel_and_split_invariance():
+    """Relabelling physical blocks gives a bitwise identical result, and a
+    sequence decoded inside the batch (split-KV) matches it decoded alone."""
+    lens = [4096] * 64
+    query, tables, caches = _setup(91, lens, 32, 8, 2048)
+    kc, vc, ks, vs = caches
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=H.DEV)
+    out = fp8_decode_attention(query.to(H.DEV), kc, vc, ks, vs, seqlens, tables.to(H.DEV), 0.088)
+    perm = torch.randperm(2048, generator=torch.Generator().manual_seed(3)).to(H.DEV)
+    inv = torch.empty_like(perm)
+    inv[perm] = torch.arange(2048, device=H.DEV)
+    kc2, vc2, ks2, vs2 = (torch.empty_like(t) for t in (kc, vc, ks, vs))
+    kc2.view(torch.uint8)[perm] = kc.view(torch.uint8)
+    vc2.view(torch.uint8)[perm] = vc.view(torch.uint8)
+    ks2[perm] = ks
+    vs2[perm] = vs
+    t2 = perm[tables.to(H.DEV).long()].to(torch.int32)
+    out2 = fp8_decode_attention(query.to(H.DEV), kc2, vc2, ks2, vs2, seqlens, t2, 0.088)
+    assert torch.equal(out, out2)
+    # the first sequence alone uses a different split count
+    solo = fp8_decode_attention(query[:1].to(H.DEV), kc, vc, ks, vs, seqlens[:1],
+                                tables[:1].to(H.DEV), 0.088)
+    assert decode_num_splits(1, 32, 8, 16, H.BLOCK) != decode_num_splits(64, 32, 8, 16, H.BLOCK)
+    assert (solo.float() - out[:1].float()).abs().max().item() < 1e-2
+
+
+def test_decode_ragged_fragmented():
+    """Ragged lengths, log-uniform in [16, 32768], blocks sampled from a
+    fragmented pool, with the one-token append stored in the same step."""
+    gen = torch.Generator().manual_seed(101)
+    b = 48
+    lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(32768), generator=gen)).long().tolist()
+    pages = sum((n + 255) // 256 for n in lens)
+    query, tables, caches = _setup(102, lens, 32, 8, pages + 97)
+    _run_and_check(query, lens, tables, caches)
+
+
+def test_decode_long_context_qwen3_32b():
+    """131072 tokens at 64 q / 8 kv heads: split-KV across the whole GPU plus
+    the log-sum-exp combine."""
+    lens = [131072]
+    query, tables, caches = _setup(111, lens, 64, 8, 512)
+    assert decode_num_splits(1, 64, 8, 512, H.BLOCK) >= 128
+    _run_and_check(query, lens, tables, caches)
+
+
+def test_decode_graph_replay_matches_eager():
+    """Capture store + decode in a HIP graph with runner-style padded inputs
+    and replay it with new contents; every replay equals the eager result."""
+    hq, hk, nb, max_bs, width = 32, 8, 64, 8, 8
+    garbage_slot = (nb - 1) * H.BLOCK
+    caches = H.alloc_cache(nb)
+    gen = torch.Generator().manual_seed(121)
+    static = dict(
+        q=torch.zeros(max_bs, hq, H.D, dtype=torch.bfloat16, device=H.DEV),
+        k=torch.zeros(max_bs, hk, H.D, dtype=torch.bfloat16, device=H.DEV),
+        v=torch.zeros(max_bs, hk, H.D, dtype=torch.bfloat16, device=H.DEV),
+        slot=torch.full((max_bs,), garbage_slot, dtype=torch.int64, device=H.DEV),
+        lens=torch.zeros(max_bs, dtype=torch.int32, device=H.DEV),
+        tables=torch.full((max_bs, width), -1, dtype=torch.int32, device=H.DEV),
+        out=torch.zeros(max_bs, hq, H.D, dtype=torch.bfloat16, device=H.DEV))
+    # prefill some history on the first 4 sequences
+    lens0 = [700, 1, 256, 1500]
+    tables, slots = H.paged_layout(gen, lens0, nb - 1)
+    n = slots.numel()
+    store_fp8_kvcache(H.randn(gen, (n, hk, H.D), torch.bfloat16).to(H.DEV),
+                      H.randn(gen, (n, hk, H.D), torch.bfloat16).to(H.DEV),
+                      *caches, slots.to(H.DEV))
+
+    def step():
+        store_fp8_kvcache(static["k"], static["v"], *caches, static["slot"])
+        fp8_decode_attention(static["q"], *caches, static["lens"], static["tables"],
+                             0.088, out=static["out"])
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    lens = list(lens0)
+    for it in range(3):
+        bs = 4
+        q = H.randn(gen, (bs, hq, H.D), torch.bfloat16)
+        k = H.randn(gen, (bs, hk, H.D), torch.bfloat16)
+        v = H.randn(gen, (bs, hk, H.D), torch.bfloat16)
+        new_slots = []
+        for b in range(bs):
+            p = lens[b]
+            new_slots.append(int(tables[b, p // H.BLOCK]) * H.BLOCK + p % H.BLOCK)
+            lens[b] += 1
+        static["q"].zero_(); static["q"][:bs] = q.to(H.DEV)
+        static["k"].zero_(); static["k"][:bs] = k.to(H.DEV)
+        static["v"].zero_(); static["v"][:bs] = v.to(H.DEV)
+        static["slot"].fill_(garbage_slot)
+        static["slot"][:bs] = torch.tensor(new_slots, device=H.DEV)
+        static["lens"].zero_(); static["lens"][:bs] = torch.tensor(lens, dtype=torch.int32, device=H.DEV)
+        static["tables"].fill_(-1); static["tables"][:bs, :tables.shape[1]] = tables.to(H.DEV)
+        snapshot = [c.clone() for c in caches]
+        graph.replay()
+        torch.cuda.synchronize()
+        got = static["out"].clone()
+        # eager on a copy of the pre-step caches
+        eager_caches = snapshot
+        store_fp8_kvcache(static["k"], static["v"], *eager_caches, static["slot"])
+        want = fp8_decode_attention(static["q"], *eager_caches, static["lens"],
+                                    static["tables"], 0.088)
+        torch.cuda.synchronize()
+        assert torch.equal(got[:bs], want[:bs]), f"replay {it}"
+        assert (got[bs:] == 0).all()
+        for a, b_ in zip(caches, eager_caches):
+            if a.dtype == torch.float8_e4m3fn:
+                same = torch.equal(a.view(torch.uint8)[: nb - 1], b_.view(torch.uint8)[: nb - 1])
+            else:
+                same = torch.equal(a[: nb - 1], b_[: nb - 1])
+            assert same, f"cache differs after replay {it}"

@@ -1,0 +1,105 @@
+"""GPU parity of the FP8-MFMA chunk / varlen prefill against the oracle
+(``fp8_chunk_prefill_attention.py:16-67``): outputs within 2e-2 max-abs and
+1e-2 relative (Frobenius) error.  The kernel quantizes q and P to e4m3 for
+the MFMAs; the oracle does neither, so these bounds measure that choice."""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import fp8_oracle as O
+from tests import gpu_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+sys.path.insert(0, GOLDEN)
+import cases  # noqa: E402
+
+from microserve_amd import (  # noqa: E402
+    fp8_chunk_prefill_attention, fp8_varlen_prefill_attention, store_fp8_kvcache)
+
+
+def test_chunk_prefill_reference_case():
+    """tests/test_fp8_kv_attention.py::test_chunk_prefill's shape: prefix 273,
+    31 queries, permuted table [[1, 0]], unscaled V."""
+    g = np.load(os.path.join(GOLDEN, "ref_shapes.npz"))
+    c = cases.chunk_case()
+    caches = H.alloc_cache(c["num_blocks"])
+    store_fp8_kvcache(c["key"].to(H.DEV), c["value"].to(H.DEV), *caches, c["slots"].to(H.DEV))
+    out = fp8_chunk_prefill_attention(c["query"].to(H.DEV), *caches, c["table"].to(H.DEV),
+                                      c["prefix"], cases.D ** -0.5)
+    ref = torch.from_numpy(g["pre_out"])
+    max_abs, rel = H.assert_attention_close(out, ref)
+    print(f"chunk prefill reference case: max_abs {max_abs:.4e} rel {rel:.4e}")
+
+
+def _varlen_setup(seed, lq, lk, hq, hk, dtype=torch.bfloat16, outliers=0.0,
+                  extra_blocks=3):
+    gen = torch.Generator().manual_seed(seed)
+    pages = sum((n + 255) // 256 for n in lk)
+    nb = pages + extra_blocks
+    tables, slots = H.paged_layout(gen, lk, nb)
+    n = slots.numel()
+    key = torch.randn(n, hk, H.D, generator=gen)
+    if outliers:
+        mask = torch.rand(n, hk, H.D, generator=gen) < outliers
+        key = torch.where(mask, key * 20, key)
+    key = key.to(dtype)
+    value = H.randn(gen, (n, hk, H.D), dtype)
+    query = H.randn(gen, (sum(lq), hq, H.D), dtype)
+    caches = H.alloc_cache(nb, H.BLOCK, hk)
+    store_fp8_kvcache(key.to(H.DEV), value.to(H.DEV), *caches, slots.to(H.DEV))
+    cu_q = torch.tensor([0] + list(np.cumsum(lq)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(lk)), dtype=torch.int32)
+    return query, tables, caches, cu_q, cu_k
+
+
+def _varlen_check(query, tables, caches, cu_q, cu_k, lq):
+    scale = H.D ** -0.5
+    out = fp8_varlen_prefill_attention(query.to(H.DEV), *caches, tables.to(H.DEV),
+                                       cu_q.to(H.DEV), cu_k.to(H.DEV), max(lq), scale)
+    torch.cuda.synchronize()
+    kc, vc, ks, vs = H.cache_to_numpy(*caches)
+    ref = O.varlen_prefill_attention(query, kc, vc, ks, vs, tables, cu_q, cu_k, scale)
+    return H.assert_attention_close(out, ref)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_varlen_prefill_mixed_batch(dtype):
+    """Cached prefixes of several lengths, a fresh sequence (prefix 0) and
+    ragged query lengths in one launch."""
+    lq = [31, 200, 1, 77, 300]
+    lk = [304, 200, 900, 77 + 513, 300 + 1024]
+    query, tables, caches, cu_q, cu_k = _varlen_setup(201, lq, lk, 32, 8, dtype)
+    _varlen_check(query, tables, caches, cu_q, cu_k, lq)
+
+
+@pytest.mark.parametrize("hq,hk", [(16, 8), (8, 8), (64, 8), (32, 2), (16, 1)])
+def test_varlen_prefill_gqa_groups(hq, hk):
+    lq = [64, 130]
+    lk = [64 + 300, 130 + 5]
+    query, tables, caches, cu_q, cu_k = _varlen_setup(211 + hq, lq, lk, hq, hk)
+    _varlen_check(query, tables, caches, cu_q, cu_k, lq)
+
+
+def test_varlen_prefill_qwen3_8b_chunk_with_outliers():
+    """A scaled Qwen3-8B chunked prefill: 2 sequences x (2048 cached + 512
+    new), 1% of K entries x20."""
+    lq = [512, 512]
+    lk = [2048 + 512, 2048 + 512]
+    query, tables, caches, cu_q, cu_k = _varlen_setup(221, lq, lk, 32, 8, outliers=0.01)
+    max_abs, rel = _varlen_check(query, tables, caches, cu_q, cu_k, lq)
+    print(f"outlier chunk prefill: max_abs {max_abs:.4e} rel {rel:.4e}")
+
+
+def test_chunk_prefill_single_equals_varlen():
+    lq, lk = [100], [100 + 700]
+    query, tables, caches, cu_q, cu_k = _varlen_setup(231, lq, lk, 32, 8)
+    a = fp8_chunk_prefill_attention(query.to(H.DEV), *caches, tables.to(H.DEV), 700, 0.088)
+    b = fp8_varlen_prefill_attention(query.to(H.DEV), *caches, tables.to(H.DEV),
+                                     cu_q.to(H.DEV), cu_k.to(H.DEV), 100, 0.088)
+    assert torch.equal(a, b)
