@@ -95,9 +95,9 @@ def time_store_fill(w, iters=5):
             "frac": store_bytes(n, HK, D) / t / 1e9 / HBM_PEAK_GBS}
 
 
-def cpu_baseline(w, budget_s=15.0):
+def cpu_baseline(w, budget_s=10.0):
     """Oracle torch-CPU decode on a bounded sample of the same workload:
-    whole sequences of the batch until about budget_s of CPU work."""
+    whole sequences of the batch, cycled until about budget_s of CPU work."""
     import numpy as np
     from oracle import fp8_oracle as O
     torch.set_num_threads(os.cpu_count() or 1)
@@ -108,17 +108,45 @@ def cpu_baseline(w, budget_s=15.0):
     tables = w["tables"][0].cpu()
     lens = np.full(BATCH, CTX)
     done, t_total = 0, 0.0
-    while done < BATCH and t_total < budget_s:
+    while t_total < budget_s and done < 16 * BATCH:
+        i = done % BATCH
         t0 = time.perf_counter()
-        O.decode_attention(q[done:done + 1], kc, vc, ks, vs, lens[done:done + 1],
-                           tables[done:done + 1], D ** -0.5)
+        O.decode_attention(q[i:i + 1], kc, vc, ks, vs, lens[i:i + 1],
+                           tables[i:i + 1], D ** -0.5)
         t_total += time.perf_counter() - t0
         done += 1
     gbs = decode_bytes(done, CTX, HQ, HK, D) / t_total / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
             "kind": "port",
-            "sample": f"{done} of {BATCH} sequences (4096 tokens each) of the "
-                      f"Qwen3-8B decode batch, torch fp32 oracle, {t_total:.1f} s"}
+            "sample": f"{done} single-sequence decodes (4096 tokens, 32 q / 8 kv heads) "
+                      f"cycling over the Qwen3-8B batch, torch fp32 oracle, {t_total:.1f} s"}
+
+
+def calibrate_copy(dev, nbytes=1 << 30, iters=5):
+    """A plain device copy of known size, for scaling the FETCH_SIZE and
+    WRITE_SIZE counters to bytes (run it under rocprofv3 --pmc)."""
+    src = torch.empty(nbytes, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(iters):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration": "torch copy_", "bytes_read_per_launch": nbytes,
+                      "bytes_written_per_launch": nbytes, "launches": iters}), flush=True)
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel calibration)."""
+    path = os.path.join(ROOT, "profiles", "decode_qwen3_8b_pmc.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1].strip()), os.path.relpath(path, ROOT)
+    except OSError:
+        pass
+    return None, None
 
 
 def main():
@@ -127,13 +155,20 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--decode-only", action="store_true",
+                    help="time decode only (no store fill timing, no CPU baseline)")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run the 1 GiB copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build runs the path on a single "
               "MI355X (multi-GPU sharding is design-only)", file=sys.stderr)
         sys.exit(2)
-    from microserve_amd import decode_num_splits, fp8_decode_attention
     dev = "cuda:0"
+    if args.calibrate_copy:
+        calibrate_copy(dev)
+        return
+    from microserve_amd import decode_num_splits, fp8_decode_attention
     w = build_workload(dev)
     torch.cuda.synchronize()
     out = torch.empty_like(w["query"])
@@ -163,7 +198,8 @@ def main():
     ms_per_step = wall / args.steps * 1e3
     value = nbytes / (wall / args.steps) / 1e9
     achieved = nbytes / avg_launch / 1e9
-    store = time_store_fill(w)
+    store = None if args.decode_only else time_store_fill(w)
+    traffic, traffic_src = measured_traffic()
     result = {
         "metric": "FP8 paged decode-attn HBM GB/s (% of peak) + store_kvcache tokens/s, Qwen3-8B",
         "value": round(value, 1),
@@ -187,10 +223,13 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(avg_launch * 1e6, 2),
                      "median_launch_us": round(per_launch[len(per_launch) // 2] * 1e6, 2),
-                     "traffic": None},
-        "store": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in store.items()},
+                     "algorithmic_bytes": nbytes,
+                     "traffic": traffic, "traffic_source": traffic_src},
     }
-    if not args.no_cpu:
+    if store is not None:
+        result["store"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                           for k, v in store.items()}
+    if not args.no_cpu and not args.decode_only:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)
 

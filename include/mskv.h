@@ -70,9 +70,14 @@ int mskv_store_fp8_kvcache(const void* key, const void* value,
 int mskv_decode_num_splits(int batch, int num_q_heads, int num_kv_heads,
                            int max_blocks_per_seq, int block_size);
 
-/* Workspace bytes mskv_fp8_decode_attention needs for num_splits (0 if 1). */
-size_t mskv_decode_workspace_bytes(int batch, int num_q_heads, int head_dim,
+/*
+ * Scratch bytes mskv_fp8_decode_attention needs for num_splits (0 if 1):
+ * the fp32 split partials.  Contents on entry do not matter.
+ */
+size_t mskv_decode_workspace_bytes(int batch, int num_q_heads,
+                                   int num_kv_heads, int head_dim,
                                    int num_splits);
+
 
 /*
  * Paged decode attention over the FP8 cache: one query token per sequence.
@@ -87,7 +92,8 @@ size_t mskv_decode_workspace_bytes(int batch, int num_q_heads, int head_dim,
  * int32 [batch]; block_tables: int32 [batch, max_blocks_per_seq], -1 padded.
  * Block ids outside [0, num_blocks) read as empty.  num_splits must be the
  * value mskv_decode_num_splits returns for the shape; when it is above 1 the
- * workspace must hold mskv_decode_workspace_bytes bytes.
+ * workspace must hold mskv_decode_workspace_bytes bytes, and a second
+ * kernel merges the split partials.
  * Supported: head_dim == 128, block_size % 32 == 0, and a GQA group
  * (num_q_heads / num_kv_heads) of at most 16 or a multiple of 16.
  */

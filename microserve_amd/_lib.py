@@ -30,7 +30,7 @@ _PROTOS = {
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int,
         _c_i64, _c_int, _c_int, _c_i64, _c_int, _vp]),
     "mskv_decode_num_splits": (_c_int, [_c_int, _c_int, _c_int, _c_int, _c_int]),
-    "mskv_decode_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int]),
+    "mskv_decode_workspace_bytes": (_c_size, [_c_int, _c_int, _c_int, _c_int, _c_int]),
     "mskv_fp8_decode_attention": (_c_int, [
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_f32,

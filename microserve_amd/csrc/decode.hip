@@ -21,10 +21,16 @@
 //    into a per-wave LDS tile and comes back transposed with
 //    ds_read_b64_tr_b8, then is converted fp8 -> bf16 in registers.
 //  * Online softmax in base 2 (v_exp_f32); the row max is a two-step xor
-//    reduction across the four lane groups that share a head.
+//    reduction (v_permlane16/32_swap, no LDS round trip) across the four
+//    lane groups that share a head, and the accumulator is rescaled lazily,
+//    only when a head's max grows by more than 2^8.
+//  * V tiles are double-buffered in LDS: step i+1's rows are staged while
+//    step i is consumed, so the V registers live only while in flight.
 //  * Split-KV: the host picks pages-per-split from shapes only; each split
 //    writes (o / l, m + log2 l) partials and decode_combine_kernel merges
-//    them.  With one split the kernel writes the output directly.
+//    them (an in-kernel merge needs agent-scope fences, i.e. an L2
+//    writeback + invalidate per XCD, which measured 2x slower).  A sequence
+//    that fits in one split is written directly by the split kernel.
 //  * Every page is read through a buffer resource sized to that page; an
 //    invalid block id gives a zero-length resource (loads return 0) and its
 //    tokens are masked, so a bad table entry cannot fault.
@@ -35,9 +41,31 @@
 
 namespace mskv {
 
+#ifndef MSKV_DECODE_TARGET_WAVES
+#define MSKV_DECODE_TARGET_WAVES 2048
+#endif
+#ifndef MSKV_DECODE_WAVES_PER_WG
+#define MSKV_DECODE_WAVES_PER_WG 8
+#endif
+#ifndef MSKV_DECODE_PREFETCH
+#define MSKV_DECODE_PREFETCH 1
+#endif
+
 constexpr int kStep = 32;          // tokens per inner step (one LDS V tile)
 constexpr int kMaxPagesPerSplit = 4;
-constexpr int kTargetWaves = 4096;
+constexpr int kTargetWaves = MSKV_DECODE_TARGET_WAVES;
+// Waves of one workgroup take consecutive kv heads of the same tokens, so a
+// workgroup streams whole contiguous token rows; the waves never synchronize
+// with each other.
+constexpr int kWavesPerWG = MSKV_DECODE_WAVES_PER_WG;
+
+// Orders this wave's LDS writes before its later LDS reads (LDS executes one
+// wave's instructions in issue order, so no workgroup barrier is needed).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -94,16 +122,26 @@ __device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
   s.valid = ok ? min(kStep, t_end - t0) : 0;
 }
 
+// 3 waves per SIMD: the register budget (<= 168 VGPRs) that holds a whole
+// step in flight without spilling
 template <typename T>
-__global__ __launch_bounds__(64) void decode_fp8_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * kWavesPerWG)
+__attribute__((amdgpu_waves_per_eu(MSKV_DECODE_PREFETCH == 2 ? 2 : 3, 8)))
+void decode_fp8_kernel(DecodeArgs a) {
   using A = Act<T>;
   using x8 = typename A::x8;
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[kStep * kHeadDim];
-  __shared__ __attribute__((aligned(16))) float s_lds[2 * kStep];
+  // per wave: two V tiles and their scales; step i is read from buffer i&1
+  // while step i+1 is staged into the other one
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds_all[kWavesPerWG][2][kStep * kHeadDim];
+  __shared__ __attribute__((aligned(16))) float s_lds_all[kWavesPerWG][2][2 * kStep];
 
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int g = lane >> 4, n = lane & 15;
-  const int unit = blockIdx.x, split = blockIdx.y, b = blockIdx.z;
+  const int unit = blockIdx.x * kWavesPerWG + wave, split = blockIdx.y, b = blockIdx.z;
+  if (unit >= a.hk * a.qgroups) return;
+  auto& v_lds = v_lds_all[wave];
+  auto& s_lds = s_lds_all[wave];
   const int kvh = unit / a.qgroups;
   const int hig = (unit - kvh * a.qgroups) * 16 + n;  // head within its group
   const bool head_ok = hig < a.group;
@@ -153,21 +191,37 @@ __global__ __launch_bounds__(64) void decode_fp8_kernel(DecodeArgs a) {
   const int trow = slot < 4 ? 4 * g + slot : 16 + 4 * g + (slot - 4);
   const uint32_t tr_base = (uint32_t)trow * kHeadDim + 8u * (i16 & 1);
 
-  StepLoads cur, nxt;
-  load_step(a, b, kvh, t_begin, t_end, lane, cur);
-  for (int t0 = t_begin; t0 < t_end; t0 += kStep) {
-    // stage V (rows past the sequence end are zeroed: their P is 0, and a
-    // stray NaN byte would otherwise poison the MFMA sum) and the scales
-    const int valid = cur.valid;
+  // Stage one step's V rows (rows past the sequence end are zeroed: their P
+  // is 0, and a stray NaN byte would otherwise poison the MFMA sum) and its
+  // scales into LDS buffer `buf`.
+  auto stage = [&](const StepLoads& s, int buf) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int row = 8 * c + (lane >> 3);
-      const u32x4 v = row < valid ? cur.v[c] : u32x4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4*>(v_lds + row * kHeadDim + 16 * (lane & 7)) = v;
+      const u32x4 v = row < s.valid ? s.v[c] : u32x4{0u, 0u, 0u, 0u};
+      *reinterpret_cast<u32x4*>(&v_lds[buf][row * kHeadDim + 16 * (lane & 7)]) = v;
     }
-    s_lds[lane] = lane < 32 ? cur.kscale : cur.vscale;
-    __syncthreads();
-    if (t0 + kStep < t_end) load_step(a, b, kvh, t0 + kStep, t_end, lane, nxt);
+    s_lds[buf][lane] = lane < 32 ? s.kscale : s.vscale;
+  };
+
+  StepLoads cur, nxt;
+  load_step(a, b, kvh, t_begin, t_end, lane, cur);
+  stage(cur, 0);
+#if MSKV_DECODE_PREFETCH == 2
+  // two steps in flight: nxt holds step i+1, far is loaded with step i+2
+  StepLoads far;
+  if (t_begin + kStep < t_end) load_step(a, b, kvh, t_begin + kStep, t_end, lane, nxt);
+#endif
+  wave_lds_sync();
+  int buf = 0;
+  for (int t0 = t_begin; t0 < t_end; t0 += kStep, buf ^= 1) {
+    const int valid = cur.valid;
+    const bool more = t0 + kStep < t_end;
+#if MSKV_DECODE_PREFETCH == 2
+    if (t0 + 2 * kStep < t_end) load_step(a, b, kvh, t0 + 2 * kStep, t_end, lane, far);
+#else
+    if (more) load_step(a, b, kvh, t0 + kStep, t_end, lane, nxt);
+#endif
 
     // S^T = K . Q^T for tokens [0,16) and [16,32) of the step
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
@@ -181,24 +235,38 @@ __global__ __launch_bounds__(64) void decode_fp8_kernel(DecodeArgs a) {
     A::fp8x4_to(cur.k1b[0], ka, 0); A::fp8x4_to(cur.k1b[1], ka, 4); s1 = A::mfma(ka, qop[2], s1);
     A::fp8x4_to(cur.k1b[2], ka, 0); A::fp8x4_to(cur.k1b[3], ka, 4); s1 = A::mfma(ka, qop[3], s1);
 
-    const f32x4 ksc0 = *reinterpret_cast<const f32x4*>(s_lds + 4 * g);
-    const f32x4 ksc1 = *reinterpret_cast<const f32x4*>(s_lds + 16 + 4 * g);
-    const f32x4 vsc0 = *reinterpret_cast<const f32x4*>(s_lds + 32 + 4 * g);
-    const f32x4 vsc1 = *reinterpret_cast<const f32x4*>(s_lds + 48 + 4 * g);
+    const float* sc = s_lds[buf];
+    const f32x4 ksc0 = *reinterpret_cast<const f32x4*>(sc + 4 * g);
+    const f32x4 ksc1 = *reinterpret_cast<const f32x4*>(sc + 16 + 4 * g);
+    const f32x4 vsc0 = *reinterpret_cast<const f32x4*>(sc + 32 + 4 * g);
+    const f32x4 vsc1 = *reinterpret_cast<const f32x4*>(sc + 48 + 4 * g);
     float x[8];
+    if (valid == kStep) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      x[r] = (4 * g + r < valid) ? s0[r] * ksc0[r] * a.scale_log2 : -INFINITY;
-      x[4 + r] = (16 + 4 * g + r < valid) ? s1[r] * ksc1[r] * a.scale_log2 : -INFINITY;
+      for (int r = 0; r < 4; ++r) {
+        x[r] = s0[r] * ksc0[r] * a.scale_log2;
+        x[4 + r] = s1[r] * ksc1[r] * a.scale_log2;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = (4 * g + r < valid) ? s0[r] * ksc0[r] * a.scale_log2 : -INFINITY;
+        x[4 + r] = (16 + 4 * g + r < valid) ? s1[r] * ksc1[r] * a.scale_log2 : -INFINITY;
+      }
     }
-    float tmax = x[0];
+    float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
+                       fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+    tmax = max_xor32(max_xor16(tmax));
+    // lazy rescale: only when some head's max outgrows the reference by the slack
+    if (__any(tmax > m + kRescaleSlack)) {
+      const float m_new = fmaxf(m, tmax);
+      const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m - m_new);
+      l *= alpha;
 #pragma unroll
-    for (int e = 1; e < 8; ++e) tmax = fmaxf(tmax, x[e]);
-    tmax = wave_max_xor(tmax, 16);
-    tmax = wave_max_xor(tmax, 32);
-    const float m_new = fmaxf(m, tmax);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2_fast(m - m_use);
+      for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      m = m_new;
+    }
+    const float m_use = m == -INFINITY ? 0.0f : m;
     float psum = 0.0f;
     bf16x8 pt;
 #pragma unroll
@@ -206,32 +274,43 @@ __global__ __launch_bounds__(64) void decode_fp8_kernel(DecodeArgs a) {
       const float p = exp2_fast(x[e] - m_use);
       psum += p;
       const float vsc = e < 4 ? vsc0[e] : vsc1[e - 4];
-      pt[e] = (__bf16)(x[e] == -INFINITY ? 0.0f : p * vsc);
+      pt[e] = (__bf16)(p * vsc);
     }
-    l = l * alpha + psum;
-    m = m_new;
+    if (valid != kStep) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] *= alpha;
+      for (int e = 0; e < 8; ++e)
+        if (x[e] == -INFINITY) pt[e] = (__bf16)0.0f;
+    }
+    l += psum;
 
     // O^T += V^T . P^T, one 16-wide d tile per MFMA
+    const uint8_t* vb = v_lds[buf];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const i32x2 raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
           reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
-              (__attribute__((address_space(3))) uint8_t*)v_lds + tr_base + 16 * dt));
+              (__attribute__((address_space(3))) uint8_t*)vb + tr_base + 16 * dt));
       const bf16x8 vt = fp8x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pt, acc[dt], 0, 0, 0);
     }
-    __syncthreads();
-    cur = nxt;
+    if (more) {
+      stage(nxt, buf ^ 1);
+      cur = nxt;
+#if MSKV_DECODE_PREFETCH == 2
+      nxt = far;
+#endif
+    }
+    wave_lds_sync();
   }
 
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
-  if (!head_ok) return;
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  if (a.splits == 1) {
-    uint16_t* op = a.out + ((int64_t)b * a.hq + qh) * kHeadDim;
+  l = sum_xor32(sum_xor16(l));
+  uint16_t* op = a.out + ((int64_t)b * a.hq + qh) * kHeadDim;
+  // splits that hold tokens of this sequence; a sequence that fits in one
+  // split is written here directly
+  const int nvalid = min(a.splits, (L + split_tokens - 1) / split_tokens);
+  if (nvalid == 1) {
+    if (!head_ok) return;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const f32x4 o = acc[dt] * inv;
@@ -239,18 +318,23 @@ __global__ __launch_bounds__(64) void decode_fp8_kernel(DecodeArgs a) {
       const uint32_t hi = (uint32_t)A::from_f32(o[2]) | ((uint32_t)A::from_f32(o[3]) << 16);
       *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{lo, hi};
     }
-  } else {
-    const int64_t row = ((int64_t)b * a.hq + qh) * a.splits + split;
-    float* po = a.part_o + row * kHeadDim;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt)
-      *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * g) = acc[dt] * inv;
-    if (g == 0) a.part_lse[row] = l > 0.0f ? m + __log2f(l) : -INFINITY;
+    return;
   }
+
+  // this split's partial: o / l and m + log2 l, merged by decode_combine_kernel
+  if (!head_ok) return;
+  const int64_t row = ((int64_t)b * a.hq + qh) * a.splits + split;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  float* po = a.part_o + row * kHeadDim;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt)
+    *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * g) = acc[dt] * inv;
+  if (g == 0) a.part_lse[row] = l > 0.0f ? m + __log2f(l) : -INFINITY;
 }
 
 // out[b, h, :] = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M) over the
-// splits that hold tokens of sequence b; zeros when there are none.
+// splits holding tokens of sequence b; zeros for an empty sequence.  Rows
+// whose sequence fits in one split were written by the split kernel.
 template <typename T>
 __global__ __launch_bounds__(64) void decode_combine_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
@@ -261,6 +345,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(
   const int lane = threadIdx.x;
   const int L = min(seqlens[b], max_tokens);
   const int nvalid = L <= 0 ? 0 : min(splits, (L + split_tokens - 1) / split_tokens);
+  if (nvalid == 1) return;
   const float* lse = part_lse + (int64_t)row * splits;
   float M = -INFINITY;
   for (int s = 0; s < nvalid; ++s) M = fmaxf(M, lse[s]);
@@ -286,13 +371,15 @@ static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
 template <typename T>
 static hipError_t launch_decode(const DecodeArgs& a, int batch,
                                 hipStream_t stream) {
-  const dim3 grid((unsigned)(a.hk * a.qgroups), (unsigned)a.splits, (unsigned)batch);
-  hipLaunchKernelGGL(decode_fp8_kernel<T>, grid, dim3(64), 0, stream, a);
+  const int units = a.hk * a.qgroups;
+  const dim3 grid((unsigned)((units + kWavesPerWG - 1) / kWavesPerWG), (unsigned)a.splits,
+                  (unsigned)batch);
+  hipLaunchKernelGGL(decode_fp8_kernel<T>, grid, dim3(64 * kWavesPerWG), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
-  hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)(batch * a.hq)),
-                     dim3(64), 0, stream, a.part_o, a.part_lse, a.seqlens,
-                     a.out, a.hq, a.splits, a.pages_per_split * a.bs, a.w * a.bs);
+  hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)(batch * a.hq)), dim3(64), 0,
+                     stream, a.part_o, a.part_lse, a.seqlens, a.out, a.hq, a.splits,
+                     a.pages_per_split * a.bs, a.w * a.bs);
   return hipGetLastError();
 }
 
@@ -320,8 +407,11 @@ extern "C" int mskv_decode_num_splits(int batch, int num_q_heads,
 }
 
 extern "C" size_t mskv_decode_workspace_bytes(int batch, int num_q_heads,
-                                              int head_dim, int num_splits) {
-  if (num_splits <= 1 || batch <= 0 || num_q_heads <= 0 || head_dim <= 0) return 0;
+                                              int num_kv_heads, int head_dim,
+                                              int num_splits) {
+  if (num_splits <= 1 || batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
+      head_dim <= 0 || num_q_heads % num_kv_heads != 0)
+    return 0;
   return (size_t)batch * num_q_heads * num_splits * (head_dim + 1) * sizeof(float);
 }
 
@@ -351,7 +441,8 @@ extern "C" int mskv_fp8_decode_attention(
   if (!query || !k_cache || !v_cache || !k_scale_cache || !v_scale_cache ||
       !cache_seqlens || !block_tables || !out)
     return MSKV_EINVAL;
-  const size_t need = mskv_decode_workspace_bytes(batch, num_q_heads, head_dim, num_splits);
+  const size_t need =
+      mskv_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, num_splits);
   if (need > 0 && (!workspace || workspace_bytes < need)) return MSKV_EWORKSPACE;
 
   mskv::DecodeArgs a;
@@ -363,8 +454,8 @@ extern "C" int mskv_fp8_decode_attention(
   a.seqlens = cache_seqlens;
   a.bt = block_tables;
   a.out = (uint16_t*)out;
-  a.part_o = (float*)workspace;
-  a.part_lse = need > 0 ? (float*)workspace + (size_t)batch * num_q_heads * num_splits * head_dim
+  a.part_o = need > 0 ? (float*)workspace : nullptr;
+  a.part_lse = need > 0 ? a.part_o + (size_t)batch * num_q_heads * num_splits * head_dim
                         : nullptr;
   a.hq = num_q_heads;
   a.hk = num_kv_heads;

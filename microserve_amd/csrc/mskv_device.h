@@ -112,6 +112,29 @@ __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c,
   return (uint32_t)w;
 }
 
+// Split four values in [-448, 448] into e4m3 hi + lo parts: hi = e4m3(y),
+// lo = e4m3(y - hi).  hi + lo carries about 8 significant bits, so an FP8
+// MFMA over both parts keeps the contraction accurate to about 2^-8.
+__device__ __forceinline__ void split_fp8x4(float a, float b, float c, float d,
+                                            uint32_t& hi, uint32_t& lo) {
+  hi = pack_fp8x4(a, b, c, d);
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false);
+  const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
+  lo = pack_fp8x4(a - h01[0], b - h01[1], c - h23[0], d - h23[1]);
+}
+
+// Three-part split: hi + mid + lo carries about 12 significant bits.
+__device__ __forceinline__ void split3_fp8x4(float a, float b, float c, float d,
+                                             uint32_t& hi, uint32_t& mid, uint32_t& lo) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  hi = pack_fp8x4(a, b, c, d);
+  const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, false);
+  const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)hi, true);
+  a -= h01[0]; b -= h01[1]; c -= h23[0]; d -= h23[1];
+  split_fp8x4(a, b, c, d, mid, lo);
+}
+
 __device__ __forceinline__ float exp2_fast(float x) {
   return __builtin_amdgcn_exp2f(x);
 }
@@ -119,5 +142,33 @@ __device__ __forceinline__ float exp2_fast(float x) {
 __device__ __forceinline__ float wave_max_xor(float v, int mask) {
   return fmaxf(v, __shfl_xor(v, mask));
 }
+
+// Cross-row exchanges without an LDS round trip.  v_permlane16_swap(x, x)
+// returns {x[l], x[l^16]} in some order on every lane, v_permlane32_swap the
+// same for l^32, so the pair's max (or sum) is the xor-16 / xor-32 reduction.
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// The running max may lag the true max by up to this many log2 units before
+// the accumulator is rescaled: exp2(x - m) then stays below 2^8.
+constexpr float kRescaleSlack = 8.0f;
 
 }  // namespace mskv

@@ -13,12 +13,15 @@
 //    waves share 128-token K/V tiles staged in LDS.
 //  * QK^T: S^T = K . Q8^T with v_mfma_f32_16x16x128_f8f6f4 -- the whole
 //    head_dim is one MFMA.  K bytes are used as stored; the query row is
-//    quantized in-kernel to e4m3 with a per-row scale, and
-//    score = acc * q_scale * k_scale * softmax_scale.
+//    quantized in-kernel with a per-row scale into e4m3 hi + mid + lo parts
+//    (q ~ hi + mid + lo to about 2^-12, so a 20x K outlier does not turn
+//    the query's rounding into visible score error), one MFMA each into the
+//    same accumulator, and score = acc * q_scale * k_scale * softmax_scale.
 //  * PV: O^T = V^T . P8^T with the same MFMA.  S^T's accumulator leaves lane
 //    (g, n) holding 32 tokens of row n, exactly the B-operand layout of P^T,
 //    so the probabilities never move between lanes.  P * v_scale is
-//    quantized to e4m3 with a per-row, per-step scale; the accumulator is
+//    quantized to e4m3 hi + lo parts with a per-row, per-step scale (two
+//    MFMAs per d tile); the accumulator is
 //    kept in units of the latest scale, so the rescale folds into the
 //    online-softmax alpha multiply.  V^T comes out of LDS transposed with
 //    ds_read_b64_tr_b8.
@@ -93,8 +96,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
   const int qh = kvh * a.group + qgi * 16 + hh;
   const int lim = row_ok ? prefix + qi + 1 : 0;
 
-  // quantize the query row: lane (g, n) holds d in [32g, 32g+32)
-  i32x8 q8;
+  // quantize the query row (hi + mid + lo e4m3 parts, one per-row scale):
+  // lane (g, n) holds d in [32g, 32g+32)
+  i32x8 q8h, q8m, q8l;
   float qscale;
   {
     float x[32];
@@ -117,8 +121,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
-    amax = wave_max_xor(amax, 16);
-    amax = wave_max_xor(amax, 32);
+    amax = max_xor32(max_xor16(amax));
     amax = fmaxf(amax, 1e-8f);
     const float inv = kFp8Max / amax;
 #pragma unroll
@@ -126,7 +129,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
       float y[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(x[4 * c + i] * inv, -kFp8Max), kFp8Max);
-      q8[c] = (int)pack_fp8x4(y[0], y[1], y[2], y[3]);
+      uint32_t h, mi, lo;
+      split3_fp8x4(y[0], y[1], y[2], y[3], h, mi, lo);
+      q8h[c] = (int)h;
+      q8m[c] = (int)mi;
+      q8l[c] = (int)lo;
     }
     qscale = amax / kFp8Max * a.scale_log2;
   }
@@ -198,7 +205,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
       const u32x4 hi = *reinterpret_cast<const u32x4*>(kp + 16);
       const i32x8 ka = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
                         (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      st[tt] = mfma_fp8(ka, q8, f32x4{0.f, 0.f, 0.f, 0.f});
+      st[tt] = mfma_fp8(ka, q8h, f32x4{0.f, 0.f, 0.f, 0.f});
+      st[tt] = mfma_fp8(ka, q8m, st[tt]);
+      st[tt] = mfma_fp8(ka, q8l, st[tt]);
     }
     // lane (g, n) now holds tokens 16*tt + 4g + r of row n
     float x[32];
@@ -215,8 +224,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
         tmax = fmaxf(tmax, v);
       }
     }
-    tmax = wave_max_xor(tmax, 16);
-    tmax = wave_max_xor(tmax, 32);
+    tmax = max_xor32(max_xor16(tmax));
     const float m_new = fmaxf(m, tmax);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float alpha = exp2_fast(m - m_use);
@@ -235,8 +243,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
         pmax = fmaxf(pmax, w);
       }
     }
-    pmax = wave_max_xor(pmax, 16);
-    pmax = wave_max_xor(pmax, 32);
+    pmax = max_xor32(max_xor16(pmax));
     const float cs_new = pmax > 0.0f ? pmax / kFp8Max : cs;
     const float f = alpha * (cs / cs_new);
 #pragma unroll
@@ -244,15 +251,18 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
     cs = cs_new;
     l = l * alpha + psum;
     m = m_new;
-    i32x8 p8;
+    i32x8 p8h, p8l;
     {
       const float pinv = pmax > 0.0f ? kFp8Max / pmax : 0.0f;
 #pragma unroll
-      for (int c = 0; c < 8; ++c)
-        p8[c] = (int)pack_fp8x4(fminf(pv[4 * c] * pinv, kFp8Max),
-                                fminf(pv[4 * c + 1] * pinv, kFp8Max),
-                                fminf(pv[4 * c + 2] * pinv, kFp8Max),
-                                fminf(pv[4 * c + 3] * pinv, kFp8Max));
+      for (int c = 0; c < 8; ++c) {
+        uint32_t h, lo;
+        split_fp8x4(fminf(pv[4 * c] * pinv, kFp8Max), fminf(pv[4 * c + 1] * pinv, kFp8Max),
+                    fminf(pv[4 * c + 2] * pinv, kFp8Max), fminf(pv[4 * c + 3] * pinv, kFp8Max),
+                    h, lo);
+        p8h[c] = (int)h;
+        p8l[c] = (int)lo;
+      }
     }
 
     // O^T += V^T . P8^T, one 16-wide d tile per MFMA
@@ -267,12 +277,12 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
         va[2 * qq] = r[0];
         va[2 * qq + 1] = r[1];
       }
-      acc[dt] = mfma_fp8(va, p8, acc[dt]);
+      acc[dt] = mfma_fp8(va, p8h, acc[dt]);
+      acc[dt] = mfma_fp8(va, p8l, acc[dt]);
     }
   }
 
-  l += __shfl_xor(l, 16);
-  l += __shfl_xor(l, 32);
+  l = sum_xor32(sum_xor16(l));
   if (!row_ok) return;
   const float scale = l > 0.0f ? cs / l : 0.0f;
   uint16_t* op = a.out + ((int64_t)(q_begin + qi) * a.hq + qh) * kHeadDim;

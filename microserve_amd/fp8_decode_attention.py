@@ -9,6 +9,20 @@ import torch
 from microserve_amd import _lib
 
 
+# Per device, the split-partials scratch, grown on demand and reused by
+# every call: decode calls on one stream (graph replays included) run one
+# after another, so they never hold it at the same time.
+_SCRATCH: dict = {}
+
+
+def _scratch(device: torch.device, nbytes: int) -> torch.Tensor:
+    buf = _SCRATCH.get(device)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _SCRATCH[device] = buf
+    return buf
+
+
 def decode_num_splits(batch_size: int, num_q_heads: int, num_kv_heads: int,
                       max_num_blocks: int, block_size: int) -> int:
     """Split-KV partition count for a decode shape (shapes only)."""
@@ -29,9 +43,10 @@ def fp8_decode_attention(
     (``fp8_decode_attention.py:62-101``), except that ``query`` may be fp16 or
     bf16 and ``block_n`` is accepted and ignored (the tile size is the
     kernel's).  The split-KV partition count depends only on shapes and the
-    partial-result workspace comes from torch's caching allocator, so the
-    call can be captured in a HIP graph.  ``out``, when given, receives the
-    result instead of a new tensor.
+    partials scratch is a persistent per-device buffer, so the call can be
+    captured in a HIP graph (calls on concurrent streams need their own
+    scratch and are not supported).
+    ``out``, when given, receives the result instead of a new tensor.
     """
     del block_n
     query = query.contiguous()
@@ -60,9 +75,8 @@ def fp8_decode_attention(
     splits = decode_num_splits(batch_size, num_q_heads, num_kv_heads,
                                max_num_blocks, block_size)
     ws_bytes = int(lib.mskv_decode_workspace_bytes(batch_size, num_q_heads,
-                                                   head_dim, splits))
-    ws = (torch.empty(ws_bytes, dtype=torch.uint8, device=query.device)
-          if ws_bytes else None)
+                                                   num_kv_heads, head_dim, splits))
+    ws = _scratch(query.device, ws_bytes) if ws_bytes else None
     status = lib.mskv_fp8_decode_attention(
         query.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
         k_scale_cache.data_ptr(), v_scale_cache.data_ptr(),

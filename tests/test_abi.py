@@ -43,15 +43,15 @@ def test_split_policy_depends_on_shapes_only():
     lib = _lib.load()
     # Qwen3-8B decode, batch 64 x 4096 tokens: 16 pages per sequence
     s = lib.mskv_decode_num_splits(64, 32, 8, 16, 256)
-    assert 1 <= s <= 16
+    assert 1 < s <= 16
     assert lib.mskv_decode_num_splits(64, 32, 8, 16, 256) == s
     # long single sequence is split across many waves, at most 4 pages each
     s = lib.mskv_decode_num_splits(1, 64, 8, 512, 256)
     assert s >= 128
     # a huge batch needs no split
     assert lib.mskv_decode_num_splits(4096, 32, 8, 4, 256) == 1
-    assert lib.mskv_decode_workspace_bytes(64, 32, 128, 1) == 0
-    assert lib.mskv_decode_workspace_bytes(64, 32, 128, 8) == 64 * 32 * 8 * 129 * 4
+    assert lib.mskv_decode_workspace_bytes(64, 32, 8, 128, 1) == 0
+    assert lib.mskv_decode_workspace_bytes(64, 32, 8, 128, 8) == 64 * 32 * 8 * 129 * 4
 
 
 def test_argument_validation_without_launch():

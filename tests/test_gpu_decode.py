@@ -238,3 +238,19 @@ def test_decode_graph_replay_matches_eager():
             else:
                 same = torch.equal(a[: nb - 1], b_[: nb - 1])
             assert same, f"cache differs after replay {it}"
+
+
+def test_decode_scratch_reuse_across_shapes():
+    """Calls of different batch sizes share the per-device partials scratch;
+    a large batch after a small one still merges its own partials."""
+    lens = [4096] * 64
+    query, tables, caches = _setup(131, lens, 32, 8, 2048)
+    q = query.to(H.DEV)
+    t = tables.to(H.DEV)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=H.DEV)
+    a = fp8_decode_attention(q, *caches, lens_d, t, 0.088)
+    small = fp8_decode_attention(q[:8], *caches, lens_d[:8], t[:8], 0.088)
+    c = fp8_decode_attention(q, *caches, lens_d, t, 0.088)
+    torch.cuda.synchronize()
+    assert torch.equal(a, c)
+    assert (small.float() - a[:8].float()).abs().max().item() < 1e-2
