@@ -8,24 +8,32 @@
 // MI355X design (one wave per (sequence, kv head, split)):
 //  * K/V are read once per kv head: the whole GQA group of q heads (up to
 //    16) rides in the N dimension of the MFMAs.
-//  * QK^T runs as S^T = K . Q^T on v_mfma_f32_16x16x32_{bf16,f16}: K rows
-//    come straight from HBM as 16-byte buffer loads (lane (g, i) holds token
-//    i, bytes [16g,16g+16) and [64+16g,64+16g+16)) and are converted to the
-//    query's 16-bit type exactly (e4m3 is a subset of fp16 and bf16); Q uses
-//    the same d permutation, so the contraction is the plain dot product.
+//  * K and V rows are read from HBM fully coalesced (eight lanes per
+//    128-byte row, streaming cache policy) and staged in a per-wave LDS
+//    tile; the MFMA operand layouts come back out of LDS.  Loading K
+//    straight into the MFMA layout puts four tokens (four lines) in every
+//    quad of lanes and measured ~8% slower.
+//  * QK^T runs as S^T = K . Q^T on v_mfma_f32_16x16x32_{bf16,f16}: lane
+//    (g, i) reads token i, bytes [16g,16g+16) and [64+16g,64+16g+16) of the
+//    K tile and converts them to the query's 16-bit type exactly (e4m3 is a
+//    subset of fp16 and bf16); Q uses the same d permutation, so the
+//    contraction is the plain dot product.
 //  * The S^T accumulator leaves lane (g, n) holding tokens {4g+r, 16+4g+r}
 //    of head n -- exactly the B-operand layout of O^T = V^T . P^T, so the
 //    probabilities never move between lanes.  P is scaled by the per-token
 //    v_scale and rounded to bf16 (fp32 range) for the PV MFMA.
-//  * V^T's A operand needs eight tokens per lane at one d: V goes row-major
-//    into a per-wave LDS tile and comes back transposed with
-//    ds_read_b64_tr_b8, then is converted fp8 -> bf16 in registers.
+//  * V^T's A operand needs eight tokens per lane at one d: it comes back
+//    out of the V tile transposed with ds_read_b64_tr_b8, then is converted
+//    fp8 -> bf16 in registers.
+//  * Tile rows are stored with their 16-byte chunks XOR-swizzled by
+//    (row / 2) % 8, which makes the row-major writes, the K reads and the
+//    transposed V reads all free of LDS bank conflicts.
 //  * Online softmax in base 2 (v_exp_f32); the row max is a two-step xor
 //    reduction (v_permlane16/32_swap, no LDS round trip) across the four
 //    lane groups that share a head, and the accumulator is rescaled lazily,
 //    only when a head's max grows by more than 2^8.
-//  * V tiles are double-buffered in LDS: step i+1's rows are staged while
-//    step i is consumed, so the V registers live only while in flight.
+//  * Tiles are double-buffered in LDS: step i+1's rows are staged while
+//    step i is consumed, so the K/V registers live only while in flight.
 //  * Split-KV: the host picks pages-per-split from shapes only; each split
 //    writes (o / l, m + log2 l) partials and decode_combine_kernel merges
 //    them (an in-kernel merge needs agent-scope fences, i.e. an L2
@@ -41,23 +49,14 @@
 
 namespace mskv {
 
-#ifndef MSKV_DECODE_TARGET_WAVES
-#define MSKV_DECODE_TARGET_WAVES 2048
-#endif
-#ifndef MSKV_DECODE_WAVES_PER_WG
-#define MSKV_DECODE_WAVES_PER_WG 8
-#endif
-#ifndef MSKV_DECODE_PREFETCH
-#define MSKV_DECODE_PREFETCH 1
-#endif
-
-constexpr int kStep = 32;          // tokens per inner step (one LDS V tile)
+constexpr int kStep = 32;  // tokens per inner step (one LDS K/V tile pair)
 constexpr int kMaxPagesPerSplit = 4;
-constexpr int kTargetWaves = MSKV_DECODE_TARGET_WAVES;
+// Split-KV aims at this many waves: eight per CU
+constexpr int kTargetWaves = 2048;
 // Waves of one workgroup take consecutive kv heads of the same tokens, so a
 // workgroup streams whole contiguous token rows; the waves never synchronize
 // with each other.
-constexpr int kWavesPerWG = MSKV_DECODE_WAVES_PER_WG;
+constexpr int kWavesPerWG = 8;
 
 // Orders this wave's LDS writes before its later LDS reads (LDS executes one
 // wave's instructions in issue order, so no workgroup barrier is needed).
@@ -84,11 +83,15 @@ struct DecodeArgs {
 };
 
 struct StepLoads {
-  u32x4 k0a, k0b, k1a, k1b;  // K rows: tile 0 (tokens 0..15), tile 1 (16..31)
-  u32x4 v[4];                // V rows 8c + lane/8, 16-byte column lane%8
-  float kscale, vscale;      // scales of token lane & 31
-  int valid;                 // tokens of this step below the sequence end
+  u32x4 k[4], v[4];      // K/V rows 8c + lane/8, 16-byte chunk lane%8
+  float kscale, vscale;  // scales of token lane & 31
+  int valid;             // tokens of this step below the sequence end
 };
+
+// LDS byte offset of 16-byte chunk `chunk` of tile row `row` (swizzled)
+__device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
+  return (uint32_t)row * kHeadDim + 16u * (uint32_t)(chunk ^ ((row >> 1) & 7));
+}
 
 __device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
                                           int t0, int t_end, int lane,
@@ -106,16 +109,11 @@ __device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
   const auto vsr = make_rsrc(a.vs + bo * a.bs * a.hk, ok ? spage_bytes : 0u);
   const uint32_t rstride = (uint32_t)a.hk * kHeadDim;
   const uint32_t base = (uint32_t)off * rstride + (uint32_t)kvh * kHeadDim;
-  const int g = lane >> 4, n = lane & 15;
-  const uint32_t kt0 = base + (uint32_t)n * rstride + 16u * g;
-  const uint32_t kt1 = kt0 + 16u * rstride;
-  s.k0a = buf_load16(kr, kt0);
-  s.k0b = buf_load16(kr, kt0 + 64u);
-  s.k1a = buf_load16(kr, kt1);
-  s.k1b = buf_load16(kr, kt1 + 64u);
-  const uint32_t vb = base + (uint32_t)(lane >> 3) * rstride + 16u * (lane & 7);
+  const uint32_t rb = base + (uint32_t)(lane >> 3) * rstride + 16u * (lane & 7);
 #pragma unroll
-  for (int c = 0; c < 4; ++c) s.v[c] = buf_load16(vr, vb + 8u * c * rstride);
+  for (int c = 0; c < 4; ++c) s.k[c] = buf_load16_nt(kr, rb + 8u * c * rstride);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) s.v[c] = buf_load16_nt(vr, rb + 8u * c * rstride);
   const uint32_t so = (((uint32_t)off + (lane & 31)) * a.hk + kvh) * 4u;
   s.kscale = buf_load_f32(ksr, so);
   s.vscale = buf_load_f32(vsr, so);
@@ -126,13 +124,13 @@ __device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
 // step in flight without spilling
 template <typename T>
 __global__ __launch_bounds__(64 * kWavesPerWG)
-__attribute__((amdgpu_waves_per_eu(MSKV_DECODE_PREFETCH == 2 ? 2 : 3, 8)))
+__attribute__((amdgpu_waves_per_eu(3, 8)))
 void decode_fp8_kernel(DecodeArgs a) {
   using A = Act<T>;
   using x8 = typename A::x8;
-  // per wave: two V tiles and their scales; step i is read from buffer i&1
-  // while step i+1 is staged into the other one
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds_all[kWavesPerWG][2][kStep * kHeadDim];
+  // per wave: two K/V tile pairs and their scales; step i is read from
+  // buffer i&1 while step i+1 is staged into the other one
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds_all[kWavesPerWG][2][2][kStep * kHeadDim];
   __shared__ __attribute__((aligned(16))) float s_lds_all[kWavesPerWG][2][2 * kStep];
 
   const int wave = threadIdx.x >> 6;
@@ -140,7 +138,7 @@ void decode_fp8_kernel(DecodeArgs a) {
   const int g = lane >> 4, n = lane & 15;
   const int unit = blockIdx.x * kWavesPerWG + wave, split = blockIdx.y, b = blockIdx.z;
   if (unit >= a.hk * a.qgroups) return;
-  auto& v_lds = v_lds_all[wave];
+  auto& kv_lds = kv_lds_all[wave];
   auto& s_lds = s_lds_all[wave];
   const int kvh = unit / a.qgroups;
   const int hig = (unit - kvh * a.qgroups) * 16 + n;  // head within its group
@@ -190,50 +188,51 @@ void decode_fp8_kernel(DecodeArgs a) {
   const int slot = i16 >> 1;
   const int trow = slot < 4 ? 4 * g + slot : 16 + 4 * g + (slot - 4);
   const uint32_t tr_base = (uint32_t)trow * kHeadDim + 8u * (i16 & 1);
+  const uint32_t tr_swz = 16u * (uint32_t)((trow >> 1) & 7);
 
-  // Stage one step's V rows (rows past the sequence end are zeroed: their P
-  // is 0, and a stray NaN byte would otherwise poison the MFMA sum) and its
-  // scales into LDS buffer `buf`.
+  // Stage one step's K/V rows and scales into LDS buffer `buf`.  V rows
+  // past the sequence end are zeroed (their P is 0, and a stray NaN byte
+  // would otherwise poison the MFMA sum); their K scores are masked.
   auto stage = [&](const StepLoads& s, int buf) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       const int row = 8 * c + (lane >> 3);
-      const u32x4 v = row < s.valid ? s.v[c] : u32x4{0u, 0u, 0u, 0u};
-      *reinterpret_cast<u32x4*>(&v_lds[buf][row * kHeadDim + 16 * (lane & 7)]) = v;
+      const uint32_t o = tile_off(row, lane & 7);
+      *reinterpret_cast<u32x4*>(&kv_lds[buf][0][o]) = s.k[c];
+      *reinterpret_cast<u32x4*>(&kv_lds[buf][1][o]) =
+          row < s.valid ? s.v[c] : u32x4{0u, 0u, 0u, 0u};
     }
     s_lds[buf][lane] = lane < 32 ? s.kscale : s.vscale;
   };
+  // K operand reads: token n (and 16 + n), chunks g and 4 + g
+  const uint32_t k_lo = tile_off(n, g), k_hi = tile_off(n, 4 + g);
 
   StepLoads cur, nxt;
   load_step(a, b, kvh, t_begin, t_end, lane, cur);
   stage(cur, 0);
-#if MSKV_DECODE_PREFETCH == 2
-  // two steps in flight: nxt holds step i+1, far is loaded with step i+2
-  StepLoads far;
-  if (t_begin + kStep < t_end) load_step(a, b, kvh, t_begin + kStep, t_end, lane, nxt);
-#endif
   wave_lds_sync();
   int buf = 0;
   for (int t0 = t_begin; t0 < t_end; t0 += kStep, buf ^= 1) {
     const int valid = cur.valid;
     const bool more = t0 + kStep < t_end;
-#if MSKV_DECODE_PREFETCH == 2
-    if (t0 + 2 * kStep < t_end) load_step(a, b, kvh, t0 + 2 * kStep, t_end, lane, far);
-#else
     if (more) load_step(a, b, kvh, t0 + kStep, t_end, lane, nxt);
-#endif
 
     // S^T = K . Q^T for tokens [0,16) and [16,32) of the step
+    const uint8_t* kt = kv_lds[buf][0];
+    const u32x4 k0a = *reinterpret_cast<const u32x4*>(kt + k_lo);
+    const u32x4 k0b = *reinterpret_cast<const u32x4*>(kt + k_hi);
+    const u32x4 k1a = *reinterpret_cast<const u32x4*>(kt + 16 * kHeadDim + k_lo);
+    const u32x4 k1b = *reinterpret_cast<const u32x4*>(kt + 16 * kHeadDim + k_hi);
     f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
     x8 ka;
-    A::fp8x4_to(cur.k0a[0], ka, 0); A::fp8x4_to(cur.k0a[1], ka, 4); s0 = A::mfma(ka, qop[0], s0);
-    A::fp8x4_to(cur.k0a[2], ka, 0); A::fp8x4_to(cur.k0a[3], ka, 4); s0 = A::mfma(ka, qop[1], s0);
-    A::fp8x4_to(cur.k0b[0], ka, 0); A::fp8x4_to(cur.k0b[1], ka, 4); s0 = A::mfma(ka, qop[2], s0);
-    A::fp8x4_to(cur.k0b[2], ka, 0); A::fp8x4_to(cur.k0b[3], ka, 4); s0 = A::mfma(ka, qop[3], s0);
-    A::fp8x4_to(cur.k1a[0], ka, 0); A::fp8x4_to(cur.k1a[1], ka, 4); s1 = A::mfma(ka, qop[0], s1);
-    A::fp8x4_to(cur.k1a[2], ka, 0); A::fp8x4_to(cur.k1a[3], ka, 4); s1 = A::mfma(ka, qop[1], s1);
-    A::fp8x4_to(cur.k1b[0], ka, 0); A::fp8x4_to(cur.k1b[1], ka, 4); s1 = A::mfma(ka, qop[2], s1);
-    A::fp8x4_to(cur.k1b[2], ka, 0); A::fp8x4_to(cur.k1b[3], ka, 4); s1 = A::mfma(ka, qop[3], s1);
+    A::fp8x4_to(k0a[0], ka, 0); A::fp8x4_to(k0a[1], ka, 4); s0 = A::mfma(ka, qop[0], s0);
+    A::fp8x4_to(k0a[2], ka, 0); A::fp8x4_to(k0a[3], ka, 4); s0 = A::mfma(ka, qop[1], s0);
+    A::fp8x4_to(k0b[0], ka, 0); A::fp8x4_to(k0b[1], ka, 4); s0 = A::mfma(ka, qop[2], s0);
+    A::fp8x4_to(k0b[2], ka, 0); A::fp8x4_to(k0b[3], ka, 4); s0 = A::mfma(ka, qop[3], s0);
+    A::fp8x4_to(k1a[0], ka, 0); A::fp8x4_to(k1a[1], ka, 4); s1 = A::mfma(ka, qop[0], s1);
+    A::fp8x4_to(k1a[2], ka, 0); A::fp8x4_to(k1a[3], ka, 4); s1 = A::mfma(ka, qop[1], s1);
+    A::fp8x4_to(k1b[0], ka, 0); A::fp8x4_to(k1b[1], ka, 4); s1 = A::mfma(ka, qop[2], s1);
+    A::fp8x4_to(k1b[2], ka, 0); A::fp8x4_to(k1b[3], ka, 4); s1 = A::mfma(ka, qop[3], s1);
 
     const float* sc = s_lds[buf];
     const f32x4 ksc0 = *reinterpret_cast<const f32x4*>(sc + 4 * g);
@@ -284,21 +283,19 @@ void decode_fp8_kernel(DecodeArgs a) {
     l += psum;
 
     // O^T += V^T . P^T, one 16-wide d tile per MFMA
-    const uint8_t* vb = v_lds[buf];
+    const uint8_t* vb = kv_lds[buf][1];
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const i32x2 raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
           reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
-              (__attribute__((address_space(3))) uint8_t*)vb + tr_base + 16 * dt));
+              (__attribute__((address_space(3))) uint8_t*)vb + tr_base +
+              ((16u * dt) ^ tr_swz)));
       const bf16x8 vt = fp8x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
       acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pt, acc[dt], 0, 0, 0);
     }
     if (more) {
       stage(nxt, buf ^ 1);
       cur = nxt;
-#if MSKV_DECODE_PREFETCH == 2
-      nxt = far;
-#endif
     }
     wave_lds_sync();
   }

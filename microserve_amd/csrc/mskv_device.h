@@ -36,6 +36,15 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r,
                             __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+// Streaming form (cache policy "nt"): for data read exactly once.  With
+// fully coalesced rows it lets the vector L1 stream lines instead of
+// holding them, which measured ~8% more decode bandwidth.
+__device__ __forceinline__ u32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r,
+                                               uint32_t off) {
+  return __builtin_bit_cast(u32x4,
+                            __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 2));
+}
+
 __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r,
                                               uint32_t off) {
   return __builtin_bit_cast(float,

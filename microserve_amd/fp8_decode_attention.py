@@ -23,6 +23,24 @@ def _scratch(device: torch.device, nbytes: int) -> torch.Tensor:
     return buf
 
 
+_PLAN: dict = {}
+
+
+def _plan(batch_size, num_q_heads, num_kv_heads, head_dim, max_num_blocks,
+          block_size):
+    """(splits, scratch bytes) for a shape, computed once per shape."""
+    key = (batch_size, num_q_heads, num_kv_heads, head_dim, max_num_blocks, block_size)
+    plan = _PLAN.get(key)
+    if plan is None:
+        lib = _lib.load()
+        splits = int(lib.mskv_decode_num_splits(batch_size, num_q_heads, num_kv_heads,
+                                                max_num_blocks, block_size))
+        ws = int(lib.mskv_decode_workspace_bytes(batch_size, num_q_heads, num_kv_heads,
+                                                 head_dim, splits))
+        plan = _PLAN[key] = (splits, ws)
+    return plan
+
+
 def decode_num_splits(batch_size: int, num_q_heads: int, num_kv_heads: int,
                       max_num_blocks: int, block_size: int) -> int:
     """Split-KV partition count for a decode shape (shapes only)."""
@@ -72,10 +90,8 @@ def fp8_decode_attention(
     else:
         assert out.shape == query.shape and out.dtype == query.dtype and out.is_contiguous()
     lib = _lib.load()
-    splits = decode_num_splits(batch_size, num_q_heads, num_kv_heads,
-                               max_num_blocks, block_size)
-    ws_bytes = int(lib.mskv_decode_workspace_bytes(batch_size, num_q_heads,
-                                                   num_kv_heads, head_dim, splits))
+    splits, ws_bytes = _plan(batch_size, num_q_heads, num_kv_heads, head_dim,
+                             max_num_blocks, block_size)
     ws = _scratch(query.device, ws_bytes) if ws_bytes else None
     status = lib.mskv_fp8_decode_attention(
         query.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
