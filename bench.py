@@ -123,6 +123,67 @@ def cpu_baseline(w, budget_s=10.0):
                       f"cycling over the Qwen3-8B batch, torch fp32 oracle, {t_total:.1f} s"}
 
 
+PRE_SEQS, PRE_CACHED, PRE_NEW = 8, 8192, 2048
+FP8_PEAK_TFLOPS = 5000.0
+
+
+def prefill_flops(seqs, cached, new, hq, d):
+    """Causal-exact QK^T + PV FLOP: query i of a sequence sees cached + i + 1
+    positions."""
+    visits = new * cached + new * (new + 1) // 2
+    return 4 * d * visits * hq * seqs
+
+
+def time_prefill(dev, iters=20, warmup=3):
+    """Varlen chunked prefill: 8 sequences x (8192 cached + 2048 new tokens),
+    32 q / 8 kv heads, bf16 q/k/v N(0,1) with 1% of K entries x20, all
+    10240 tokens of each sequence stored first (as Attention does)."""
+    from microserve_amd import fp8_varlen_prefill_attention, store_fp8_kvcache
+    gen = torch.Generator().manual_seed(77)
+    lk = PRE_CACHED + PRE_NEW
+    pages = lk // BS
+    pool = PRE_SEQS * pages + 1
+    perm = torch.randperm(pool, generator=gen)[:PRE_SEQS * pages].to(torch.int32)
+    tables = perm.view(PRE_SEQS, pages).contiguous()
+    pos = torch.arange(lk)
+    slots = (tables[:, pos // BS].long() * BS + pos % BS).reshape(-1)
+    key = torch.randn(slots.numel(), HK, D, generator=gen)
+    key = torch.where(torch.rand(key.shape, generator=gen) < 0.01, key * 20, key).bfloat16()
+    value = torch.randn(slots.numel(), HK, D, generator=gen).bfloat16()
+    kc = torch.zeros(pool, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(pool, BS, HK, device=dev)
+    vs = torch.ones_like(ks)
+    store_fp8_kvcache(key.to(dev), value.to(dev), kc, vc, ks, vs, slots.to(dev))
+    q = torch.randn(PRE_SEQS * PRE_NEW, HQ, D, generator=gen).bfloat16().to(dev)
+    cu_q = torch.arange(0, PRE_SEQS + 1, dtype=torch.int32, device=dev) * PRE_NEW
+    cu_k = torch.arange(0, PRE_SEQS + 1, dtype=torch.int32, device=dev) * lk
+    tables = tables.to(dev)
+
+    def run():
+        return fp8_varlen_prefill_attention(q, kc, vc, ks, vs, tables, cu_q, cu_k,
+                                            PRE_NEW, D ** -0.5)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
+    for e0, e1 in evs:
+        e0.record(stream)
+        run()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
+    flop = prefill_flops(PRE_SEQS, PRE_CACHED, PRE_NEW, HQ, D)
+    tflops = flop / us / 1e6
+    return {"workload": "varlen chunked prefill, 8 seqs x (8192 cached + 2048 new), "
+                        "32 q / 8 kv heads, fp8 cache, bf16 q",
+            "us": round(us, 2), "flop": flop, "tflops": round(tflops, 1),
+            "peak_tflops": FP8_PEAK_TFLOPS, "frac": round(tflops / FP8_PEAK_TFLOPS, 4)}
+
+
 def calibrate_copy(dev, nbytes=1 << 30, iters=5):
     """A plain device copy of known size, for scaling the FETCH_SIZE and
     WRITE_SIZE counters to bytes (run it under rocprofv3 --pmc)."""
@@ -158,6 +219,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--decode-only", action="store_true",
                     help="time decode only (no store fill timing, no CPU baseline)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="time only the varlen chunked prefill workload")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run the 1 GiB copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
@@ -168,6 +231,9 @@ def main():
     dev = "cuda:0"
     if args.calibrate_copy:
         calibrate_copy(dev)
+        return
+    if args.prefill_only:
+        print(json.dumps({"prefill": time_prefill(dev)}))
         return
     from microserve_amd import decode_num_splits, fp8_decode_attention
     w = build_workload(dev)
@@ -235,6 +301,8 @@ def main():
     if store is not None:
         result["store"] = {k: (round(v, 4) if isinstance(v, float) else v)
                            for k, v in store.items()}
+    if not args.decode_only:
+        result["prefill"] = time_prefill(dev)
     if not args.no_cpu and not args.decode_only:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)

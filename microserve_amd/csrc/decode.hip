@@ -88,10 +88,6 @@ struct StepLoads {
   int valid;             // tokens of this step below the sequence end
 };
 
-// LDS byte offset of 16-byte chunk `chunk` of tile row `row` (swizzled)
-__device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
-  return (uint32_t)row * kHeadDim + 16u * (uint32_t)(chunk ^ ((row >> 1) & 7));
-}
 
 __device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
                                           int t0, int t_end, int lane,

@@ -51,6 +51,15 @@ __device__ __forceinline__ float buf_load_f32(__amdgpu_buffer_rsrc_t r,
                             __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
 }
 
+// LDS byte offset of 16-byte chunk `chunk` of row `row` in a tile of
+// 128-byte rows, XOR-swizzled by (row / 2) % 8.  Row-major writes of eight
+// chunks per row, reads of one chunk from 16 consecutive rows (MFMA operand
+// rows), and ds_read_b64_tr_b8 reads of one chunk from 32 consecutive rows
+// all spread evenly over the 64 LDS banks.
+__device__ __forceinline__ uint32_t tile_off(int row, int chunk) {
+  return (uint32_t)row * kHeadDim + 16u * (uint32_t)(chunk ^ ((row >> 1) & 7));
+}
+
 // ------------------------------------------------------- activation types --
 // Two instantiations of one code path: fp16 and bf16 activations.
 template <typename T>

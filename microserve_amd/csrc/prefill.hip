@@ -7,26 +7,34 @@
 // block_tables[s][p / BS] * BS + p % BS.
 //
 // MI355X design:
-//  * A workgroup is four waves.  Each wave owns 16 rows; a row is one
-//    (query token, q head) pair and the GQA group of one kv head fills the
-//    rows, so one K/V tile serves every q head that reads it.  The four
-//    waves share 128-token K/V tiles staged in LDS.
+//  * A workgroup is four waves over one (sequence, kv head, block of query
+//    tokens).  A row is one (query token, q head) pair; the GQA group of the
+//    kv head fills the rows, so every K/V tile serves all the q heads that
+//    read it.  Each wave owns two 16-row blocks: every K and V operand it
+//    reads from LDS feeds both, which halves LDS traffic per FLOP.
+//  * K/V tiles of 128 keys (one f8f6f4 MFMA contraction) are staged in LDS,
+//    double-buffered with one barrier per tile.  Rows are written with their
+//    16-byte chunks XOR-swizzled by (row / 2) % 8, which keeps the row
+//    writes, the K operand reads and the transposed V reads free of bank
+//    conflicts.
 //  * QK^T: S^T = K . Q8^T with v_mfma_f32_16x16x128_f8f6f4 -- the whole
-//    head_dim is one MFMA.  K bytes are used as stored; the query row is
-//    quantized in-kernel with a per-row scale into e4m3 hi + mid + lo parts
-//    (q ~ hi + mid + lo to about 2^-12, so a 20x K outlier does not turn
-//    the query's rounding into visible score error), one MFMA each into the
-//    same accumulator, and score = acc * q_scale * k_scale * softmax_scale.
+//    head_dim is one MFMA.  K bytes are used as stored.  The query row is
+//    scaled by a power of two (exact) and split into e4m3 parts: hi + lo
+//    represent a bf16 query exactly (4 + 4 significant bits), fp16 needs
+//    hi + mid + lo; one MFMA per part into the same accumulator.
 //  * PV: O^T = V^T . P8^T with the same MFMA.  S^T's accumulator leaves lane
-//    (g, n) holding 32 tokens of row n, exactly the B-operand layout of P^T,
-//    so the probabilities never move between lanes.  P * v_scale is
-//    quantized to e4m3 hi + lo parts with a per-row, per-step scale (two
-//    MFMAs per d tile); the accumulator is
-//    kept in units of the latest scale, so the rescale folds into the
-//    online-softmax alpha multiply.  V^T comes out of LDS transposed with
-//    ds_read_b64_tr_b8.
-//  * Pages are read through page-sized buffer resources; an invalid block
-//    id gives zero-length reads and its tokens are masked.
+//    (g, n) holding 32 keys of row n, exactly the B-operand layout of P^T,
+//    so probabilities never move between lanes; V^T comes out of LDS with
+//    ds_read_b64_tr_b8.  P * v_scale is split into e4m3 hi + lo parts after
+//    a per-tile power-of-two scale chosen from the tile's largest v_scale;
+//    the accumulator is rescaled (exactly) only when that power changes.
+//  * Online softmax in base 2 with a lazy rescale: the accumulator is
+//    rescaled only when some row's max grows by more than 2^2.  Masks are
+//    evaluated only on tiles that straddle the causal diagonal or the end
+//    of the keys; fully visible tiles skip them.
+//  * Query blocks are launched last-first, so the longest workgroups start
+//    first.  Pages are read through page-sized buffer resources; an
+//    invalid block id gives zero-length reads and its keys are masked.
 #include <math.h>
 
 #include "mskv_device.h"
@@ -34,9 +42,22 @@
 
 namespace mskv {
 
-constexpr int kPStep = 128;   // tokens per K/V tile
+constexpr int kPStep = 128;  // keys per tile
 constexpr int kPWaves = 4;
+constexpr int kPBlocks = 2;  // 16-row blocks per wave
 constexpr int kPThreads = 64 * kPWaves;
+// The running max may lag a row's true max by up to kPSlack (log2 units)
+// before the accumulator is rescaled, so p = exp2(x - m) <= 2^kPSlack.  The
+// tile's v_scales are scaled to at most kPVScaleMax, which keeps p * v_scale
+// within e4m3's 448 and puts p = 1 near 100: probabilities down to ~2^-8
+// keep both of their e4m3 parts in the normal range.  (A slack of 2^8 put
+// p = 1 near 1.5 and measured 2.2e-2 max-abs error with 1% x20 K outliers.)
+constexpr float kPSlack = 2.0f;
+constexpr float kPVScaleMax = 96.0f;
+
+// e4m3 parts the query is split into: a bf16 value has 8 significant bits
+template <typename T> struct QuerySplit { static constexpr int parts = 3; };
+template <> struct QuerySplit<__bf16> { static constexpr int parts = 2; };
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -60,16 +81,39 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, f32x4 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+// largest power of two <= x, for a positive normal x
+__device__ __forceinline__ float pow2_floor(float x) {
+  return __uint_as_float(__float_as_uint(x) & 0xFF800000u);
+}
+
+// Direct global -> LDS loads (buffer_load ... lds): lane i of the wave
+// writes its `bytes` at lds + i * bytes, from any per-lane offset.
+__device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)lds, 16, (int)off, 0, 0, 0);
+}
+__device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      r, (__attribute__((address_space(3))) void*)lds, 4, (int)off, 0, 0, 0);
+}
+
 template <typename T>
-__global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPThreads, 2) void prefill_fp8_kernel(PrefillArgs a) {
   using A = Act<T>;
-  __shared__ __attribute__((aligned(16))) uint8_t k_lds[kPStep * kHeadDim];
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[kPStep * kHeadDim];
-  __shared__ __attribute__((aligned(16))) float ks_lds[kPStep];
-  __shared__ __attribute__((aligned(16))) float vs_lds[kPStep];
+  constexpr int NQ = QuerySplit<T>::parts;
+  // two tile buffers as separate objects, and a loop unrolled by two, so
+  // the compiler can see that the direct loads into one buffer never alias
+  // the reads of the other (otherwise it waits for them before every read)
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds0[kPStep * kHeadDim];
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds0[kPStep * kHeadDim];
+  __shared__ __attribute__((aligned(16))) uint8_t k_lds1[kPStep * kHeadDim];
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds1[kPStep * kHeadDim];
+  __shared__ __attribute__((aligned(16))) float sc_lds0[2][kPStep];
+  __shared__ __attribute__((aligned(16))) float sc_lds1[2][kPStep];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int g = lane >> 4, n = lane & 15;
   const int s = blockIdx.z;
   const int unit = blockIdx.y;
@@ -84,30 +128,38 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
   const int lq = q_end - q_begin;
   const int lk = a.cu_k ? a.cu_k[s + 1] - a.cu_k[s] : a.prefix_len + lq;
   const int prefix = lk - lq;
-  const int wg_q0 = blockIdx.x * kPWaves * a.tpr;
+  const int wave_tok = kPBlocks * a.tpr;  // query tokens per wave
+  const int wg_tok = kPWaves * wave_tok;
+  const int wg_q0 = (int)(gridDim.x - 1 - blockIdx.x) * wg_tok;
   if (wg_q0 >= lq || lq <= 0) return;
-  const int wg_qlast = min(lq, wg_q0 + kPWaves * a.tpr) - 1;
+  const int wg_qlast = min(lq, wg_q0 + wg_tok) - 1;
   const int kv_end = min(min(lk, prefix + wg_qlast + 1), a.w * a.bs);
+  // keys below w_all are visible to every row of this wave; no row of it
+  // sees keys at or above w_none
+  const int w_q0 = wg_q0 + wave * wave_tok;
+  const int w_all = prefix + w_q0 + 1;
+  const int w_none = w_q0 < lq ? prefix + min(lq, w_q0 + wave_tok) : 0;
 
-  // this lane's row: query token wg_q0 + wave*tpr + n/gc, head n%gc of the group
-  const int qi = wg_q0 + wave * a.tpr + n / a.gc;
-  const int hh = n % a.gc;
-  const bool row_ok = n < a.tpr * a.gc && qi < lq;
-  const int qh = kvh * a.group + qgi * 16 + hh;
-  const int lim = row_ok ? prefix + qi + 1 : 0;
-
-  // quantize the query row (hi + mid + lo e4m3 parts, one per-row scale):
-  // lane (g, n) holds d in [32g, 32g+32)
-  i32x8 q8h, q8m, q8l;
-  float qscale;
-  {
+  // rows: block b, lane n -> query token w_q0 + b * tpr + n / gc, head n % gc
+  int lim[kPBlocks];
+  bool row_ok[kPBlocks];
+  int qh[kPBlocks];
+  i32x8 qp[kPBlocks][NQ];
+  float qs[kPBlocks];
+#pragma unroll
+  for (int b = 0; b < kPBlocks; ++b) {
+    const int qi = w_q0 + b * a.tpr + n / a.gc;
+    row_ok[b] = n < a.tpr * a.gc && qi < lq;
+    qh[b] = kvh * a.group + qgi * 16 + n % a.gc;
+    lim[b] = row_ok[b] ? prefix + qi + 1 : 0;
+    // lane (g, n) holds d in [32g, 32g+32) of its row
     float x[32];
-    if (row_ok) {
-      const u32x4* qp = reinterpret_cast<const u32x4*>(
-          a.q + ((int64_t)(q_begin + qi) * a.hq + qh) * kHeadDim + 32 * g);
+    if (row_ok[b]) {
+      const u32x4* qp4 = reinterpret_cast<const u32x4*>(
+          a.q + ((int64_t)(q_begin + qi) * a.hq + qh[b]) * kHeadDim + 32 * g);
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        const u32x4 v = qp[c];
+        const u32x4 v = qp4[c];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           x[8 * c + 2 * i] = A::to_f32((uint16_t)(v[i] & 0xFFFFu));
@@ -122,176 +174,265 @@ __global__ __launch_bounds__(kPThreads) void prefill_fp8_kernel(PrefillArgs a) {
 #pragma unroll
     for (int i = 0; i < 32; ++i) amax = fmaxf(amax, fabsf(x[i]));
     amax = max_xor32(max_xor16(amax));
-    amax = fmaxf(amax, 1e-8f);
-    const float inv = kFp8Max / amax;
+    // power-of-two scale: x * f is exact, so the parts carry every bit
+    const float f = amax > 1e-30f ? pow2_floor(kFp8Max / amax) : 1.0f;
+    qs[b] = a.scale_log2 / f;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
       float y[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(x[4 * c + i] * inv, -kFp8Max), kFp8Max);
+      for (int i = 0; i < 4; ++i) y[i] = fminf(fmaxf(x[4 * c + i] * f, -kFp8Max), kFp8Max);
       uint32_t h, mi, lo;
-      split3_fp8x4(y[0], y[1], y[2], y[3], h, mi, lo);
-      q8h[c] = (int)h;
-      q8m[c] = (int)mi;
-      q8l[c] = (int)lo;
+      if constexpr (NQ == 2) {
+        split_fp8x4(y[0], y[1], y[2], y[3], h, lo);
+        qp[b][0][c] = (int)h;
+        qp[b][1][c] = (int)lo;
+      } else {
+        split3_fp8x4(y[0], y[1], y[2], y[3], h, mi, lo);
+        qp[b][0][c] = (int)h;
+        qp[b][1][c] = (int)mi;
+        qp[b][2][c] = (int)lo;
+      }
     }
-    qscale = amax / kFp8Max * a.scale_log2;
   }
 
-  f32x4 acc[8];
+  f32x4 acc[kPBlocks][8];
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.0f, cs = 1.0f;
+  for (int b = 0; b < kPBlocks; ++b)
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[b][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[kPBlocks], l[kPBlocks];
+#pragma unroll
+  for (int b = 0; b < kPBlocks; ++b) {
+    m[b] = -INFINITY;
+    l[b] = 0.0f;
+  }
+  float fcur = 0.0f;  // power-of-two scale of p * v_scale in acc (0: none yet)
 
-  // ds_read_b64_tr_b8 address of this lane for read q (tokens 8q..8q+7 of
-  // the lane group's 32): token slot e = 8q + i/2 maps to step row
-  // 16*(e/4) + 4g + e%4, column half i%2.
+  // K operand: key n of each 16-key group, 16-byte chunks 2g and 2g + 1;
+  // the swizzle of rows 16t + n does not depend on t
+  const uint32_t k_lo = tile_off(n, 2 * g), k_hi = tile_off(n, 2 * g + 1);
+  // ds_read_b64_tr_b8 address of this lane for read qq (keys 8qq..8qq+7 of
+  // the lane group's 32): key slot e = 8qq + i/2 maps to tile row
+  // 16*(e/4) + 4g + e%4, column half i%2
   const int i16 = lane & 15;
-  uint32_t tr_addr[4];
+  uint32_t tr_row[4], tr_swz[4];
 #pragma unroll
   for (int qq = 0; qq < 4; ++qq) {
     const int e = 8 * qq + (i16 >> 1);
     const int row = 16 * (e >> 2) + 4 * g + (e & 3);
-    tr_addr[qq] = (uint32_t)row * kHeadDim + 8u * (i16 & 1);
+    tr_row[qq] = (uint32_t)row * kHeadDim + 8u * (i16 & 1);
+    tr_swz[qq] = 16u * (uint32_t)((row >> 1) & 7);
   }
 
   const uint32_t page_bytes = (uint32_t)a.bs * a.hk * kHeadDim;
   const uint32_t spage_bytes = (uint32_t)a.bs * a.hk * 4u;
   const uint32_t rstride = (uint32_t)a.hk * kHeadDim;
+  // the block table is read-only: the constant address space keeps its
+  // loads scalar
+  const auto* btc = reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(
+      reinterpret_cast<uintptr_t>(a.bt));
 
-  for (int t0 = 0; t0 < kv_end; t0 += kPStep) {
+  // Stage tile t0 into LDS buffer `buf` with direct loads; returns the
+  // number of keys holding real tokens.  Wave w's j-th K (and V) load fills
+  // tile rows 8(4j + w) .. +8: lane i lands in slot i of that kilobyte, i.e.
+  // row 8(4j + w) + i/8 at swizzled position i%8, so it reads logical chunk
+  // (i%8) ^ swizzle(row); four consecutive lanes still read one aligned
+  // 64-byte half row.  The resources end at the last valid row, so rows past
+  // it read as zeros (a stray NaN byte would otherwise poison the MFMA sum)
+  // and so do their scales.
+  auto stage_tile = [&](int t0, uint8_t* kt, uint8_t* vt, float (*sct)[kPStep]) {
     const int page = t0 / a.bs;
     const int off = t0 - page * a.bs;
-    const int blk = a.bt[(int64_t)s * a.w + page];
+    const int blk = btc[(int64_t)s * a.w + page];
     const bool ok = blk >= 0 && (int64_t)blk < a.num_blocks;
+    const int valid = ok ? min(kPStep, lk - t0) : 0;
     const int64_t bo = ok ? blk : 0;
-    const auto kr = make_rsrc(a.kc + bo * page_bytes, ok ? page_bytes : 0u);
-    const auto vr = make_rsrc(a.vc + bo * page_bytes, ok ? page_bytes : 0u);
-    const auto ksr = make_rsrc(a.ks + bo * a.bs * a.hk, ok ? spage_bytes : 0u);
-    const auto vsr = make_rsrc(a.vs + bo * a.bs * a.hk, ok ? spage_bytes : 0u);
-    const int valid = ok ? min(kPStep, lk - t0) : 0;  // rows holding real tokens
-
-    // cooperative tile load: 1024 16-byte chunks of K and of V
-    u32x4 kv[4], vv[4];
+    const uint32_t kv_bytes = (uint32_t)(off + valid) * rstride;
+    const auto kr = make_rsrc(a.kc + bo * page_bytes, valid > 0 ? kv_bytes : 0u);
+    const auto vr = make_rsrc(a.vc + bo * page_bytes, valid > 0 ? kv_bytes : 0u);
+    const auto sr = make_rsrc((wave < 2 ? a.ks : a.vs) + bo * a.bs * a.hk,
+                              valid > 0 ? (uint32_t)(off + valid) * a.hk * 4u : 0u);
     const uint32_t base = (uint32_t)off * rstride + (uint32_t)kvh * kHeadDim;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int c = tid + kPThreads * j;
-      const uint32_t o = base + (uint32_t)(c >> 3) * rstride + 16u * (c & 7);
-      kv[j] = buf_load16(kr, o);
-      vv[j] = buf_load16(vr, o);
+      const int row = 8 * (4 * j + wave) + (lane >> 3);
+      const int c = (lane & 7) ^ ((row >> 1) & 7);
+      const uint32_t o = base + (uint32_t)row * rstride + 16u * c;
+      lds_load16(kr, kt + 1024 * (4 * j + wave), o);
+      lds_load16(vr, vt + 1024 * (4 * j + wave), o);
     }
-    const uint32_t so = (((uint32_t)off + (tid & (kPStep - 1))) * a.hk + kvh) * 4u;
-    const float sc = tid < kPStep ? buf_load_f32(ksr, so) : buf_load_f32(vsr, so);
-    __syncthreads();  // the previous tile is no longer read
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int c = tid + kPThreads * j;
-      const int row = c >> 3;
-      *reinterpret_cast<u32x4*>(k_lds + row * kHeadDim + 16 * (c & 7)) = kv[j];
-      *reinterpret_cast<u32x4*>(v_lds + row * kHeadDim + 16 * (c & 7)) =
-          row < valid ? vv[j] : u32x4{0u, 0u, 0u, 0u};
-    }
-    if (tid < kPStep) ks_lds[tid] = sc;
-    else vs_lds[tid - kPStep] = sc;
-    __syncthreads();
+    const int key = 64 * (wave & 1) + lane;
+    lds_load4(sr, &sct[wave >> 1][64 * (wave & 1)],
+             (((uint32_t)off + key) * a.hk + kvh) * 4u);
+    return valid;
+  };
 
-    // S^T = K . Q8^T, eight 16-token tiles
-    f32x4 st[8];
+  // one tile of work for this wave: QK^T, softmax, PV
+  auto compute_tile = [&](int t0, int valid, const uint8_t* kt, const uint8_t* vt,
+                          const float (*sct)[kPStep]) {
+    if (t0 < w_none) {
+      const float* kss = sct[0];
+      const float* vss = sct[1];
+      // S^T = K . Q8^T: lane (g, n) gets keys 16tt + 4g + r of row n
+      f32x4 st[kPBlocks][8];
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      const uint8_t* kp = k_lds + (16 * tt + n) * kHeadDim + 32 * g;
-      const u32x4 lo = *reinterpret_cast<const u32x4*>(kp);
-      const u32x4 hi = *reinterpret_cast<const u32x4*>(kp + 16);
-      const i32x8 ka = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
-                        (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
-      st[tt] = mfma_fp8(ka, q8h, f32x4{0.f, 0.f, 0.f, 0.f});
-      st[tt] = mfma_fp8(ka, q8m, st[tt]);
-      st[tt] = mfma_fp8(ka, q8l, st[tt]);
-    }
-    // lane (g, n) now holds tokens 16*tt + 4g + r of row n
-    float x[32];
-    float tmax = -INFINITY;
+      for (int tt = 0; tt < 8; ++tt) {
+        const u32x4 lo = *reinterpret_cast<const u32x4*>(kt + 16 * tt * kHeadDim + k_lo);
+        const u32x4 hi = *reinterpret_cast<const u32x4*>(kt + 16 * tt * kHeadDim + k_hi);
+        const i32x8 ka = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                          (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      const f32x4 ksc = *reinterpret_cast<const f32x4*>(ks_lds + 16 * tt + 4 * g);
+        for (int b = 0; b < kPBlocks; ++b) {
+          st[b][tt] = mfma_fp8(ka, qp[b][0], f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * tt + 4 * g + r;
-        const bool vis = row < valid && t0 + row < lim;
-        const float v = vis ? st[tt][r] * ksc[r] * qscale : -INFINITY;
-        x[4 * tt + r] = v;
-        tmax = fmaxf(tmax, v);
+          for (int p = 1; p < NQ; ++p) st[b][tt] = mfma_fp8(ka, qp[b][p], st[b][tt]);
+        }
+      }
+      // s * k_scale; masked keys -> -inf on tiles that need masks
+      const bool full = t0 + kPStep <= w_all && valid == kPStep;
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt) {
+        const f32x4 ksc = *reinterpret_cast<const f32x4*>(kss + 16 * tt + 4 * g);
+#pragma unroll
+        for (int b = 0; b < kPBlocks; ++b) st[b][tt] *= ksc;
+      }
+      if (!full) {
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int key = 16 * tt + 4 * g + r;
+#pragma unroll
+            for (int b = 0; b < kPBlocks; ++b)
+              if (!(key < valid && t0 + key < lim[b])) st[b][tt][r] = -INFINITY;
+          }
+      }
+      // row maxima in log2 units (qs > 0 per row)
+      float tm[kPBlocks];
+#pragma unroll
+      for (int b = 0; b < kPBlocks; ++b) {
+        float v = -INFINITY;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
+          v = fmaxf(v, fmaxf(fmaxf(st[b][tt][0], st[b][tt][1]), fmaxf(st[b][tt][2], st[b][tt][3])));
+        tm[b] = max_xor32(max_xor16(v)) * qs[b];
+      }
+      bool grow = false;
+#pragma unroll
+      for (int b = 0; b < kPBlocks; ++b) grow |= tm[b] > m[b] + kPSlack;
+      if (__any(grow)) {
+#pragma unroll
+        for (int b = 0; b < kPBlocks; ++b) {
+          const float m_new = fmaxf(m[b], tm[b]);
+          const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[b] - m_new);
+          l[b] *= alpha;
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= alpha;
+          m[b] = m_new;
+        }
+      }
+      // this tile's power-of-two scale for p * v_scale, from its largest
+      // v_scale (lane group g reads keys 16tt + 4g + r)
+      float vm = 0.0f;
+#pragma unroll
+      for (int tt = 0; tt < 8; ++tt) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
+        vm = fmaxf(vm, fmaxf(fmaxf(v4[0], v4[1]), fmaxf(v4[2], v4[3])));
+      }
+      vm = max_xor32(max_xor16(vm));
+      if (vm > 0.0f) {
+        const float ft = pow2_floor(kPVScaleMax / vm);
+        if (ft != fcur) {
+          if (fcur > 0.0f) {
+            const float r = ft / fcur;  // a power of two: exact
+#pragma unroll
+            for (int b = 0; b < kPBlocks; ++b)
+#pragma unroll
+              for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= r;
+          }
+          fcur = ft;
+        }
+      }
+      // P8 = e4m3 hi + lo of p * v_scale * fcur, p = exp2(x * qs - m)
+      i32x8 p8h[kPBlocks], p8l[kPBlocks];
+#pragma unroll
+      for (int b = 0; b < kPBlocks; ++b) {
+        const float m_use = m[b] == -INFINITY ? 0.0f : m[b];
+        float psum = 0.0f;
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) {
+          const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g) * fcur;
+          float y[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float p = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use));
+            psum += p;
+            y[r] = p * vsc[r];
+          }
+          uint32_t h, lo;
+          split_fp8x4(y[0], y[1], y[2], y[3], h, lo);
+          p8h[b][tt] = (int)h;
+          p8l[b][tt] = (int)lo;
+        }
+        l[b] += psum;
+      }
+      // O^T += V^T . P8^T, one 16-wide d tile per MFMA pair
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        i32x8 va;
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
+                  (__attribute__((address_space(3))) uint8_t*)vt + tr_row[qq] +
+                  ((16u * dt) ^ tr_swz[qq])));
+          va[2 * qq] = r[0];
+          va[2 * qq + 1] = r[1];
+        }
+#pragma unroll
+        for (int b = 0; b < kPBlocks; ++b) {
+          acc[b][dt] = mfma_fp8(va, p8h[b], acc[b][dt]);
+          acc[b][dt] = mfma_fp8(va, p8l[b], acc[b][dt]);
+        }
       }
     }
-    tmax = max_xor32(max_xor16(tmax));
-    const float m_new = fmaxf(m, tmax);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2_fast(m - m_use);
-    float psum = 0.0f, pmax = 0.0f;
-    float pv[32];
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      const f32x4 vsc = *reinterpret_cast<const f32x4*>(vs_lds + 16 * tt + 4 * g);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int e = 4 * tt + r;
-        const float p = exp2_fast(x[e] - m_use);
-        psum += p;
-        const float w = x[e] == -INFINITY ? 0.0f : p * vsc[r];
-        pv[e] = w;
-        pmax = fmaxf(pmax, w);
-      }
-    }
-    pmax = max_xor32(max_xor16(pmax));
-    const float cs_new = pmax > 0.0f ? pmax / kFp8Max : cs;
-    const float f = alpha * (cs / cs_new);
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[dt] *= f;
-    cs = cs_new;
-    l = l * alpha + psum;
-    m = m_new;
-    i32x8 p8h, p8l;
+  };
+
+  int valid = stage_tile(0, k_lds0, v_lds0, sc_lds0);
+  __syncthreads();
+  for (int t0 = 0; t0 < kv_end; t0 += 2 * kPStep) {
     {
-      const float pinv = pmax > 0.0f ? kFp8Max / pmax : 0.0f;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        uint32_t h, lo;
-        split_fp8x4(fminf(pv[4 * c] * pinv, kFp8Max), fminf(pv[4 * c + 1] * pinv, kFp8Max),
-                    fminf(pv[4 * c + 2] * pinv, kFp8Max), fminf(pv[4 * c + 3] * pinv, kFp8Max),
-                    h, lo);
-        p8h[c] = (int)h;
-        p8l[c] = (int)lo;
-      }
+      const bool more = t0 + kPStep < kv_end;
+      const int valid_next = more ? stage_tile(t0 + kPStep, k_lds1, v_lds1, sc_lds1) : 0;
+      compute_tile(t0, valid, k_lds0, v_lds0, sc_lds0);
+      __syncthreads();  // also waits for this wave's direct loads
+      valid = valid_next;
+      if (!more) break;
     }
-
-    // O^T += V^T . P8^T, one 16-wide d tile per MFMA
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      i32x8 va;
-#pragma unroll
-      for (int qq = 0; qq < 4; ++qq) {
-        const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-            reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
-                (__attribute__((address_space(3))) uint8_t*)v_lds + tr_addr[qq] + 16 * dt));
-        va[2 * qq] = r[0];
-        va[2 * qq + 1] = r[1];
-      }
-      acc[dt] = mfma_fp8(va, p8h, acc[dt]);
-      acc[dt] = mfma_fp8(va, p8l, acc[dt]);
+    {
+      const int t1 = t0 + kPStep;
+      const bool more = t1 + kPStep < kv_end;
+      const int valid_next = more ? stage_tile(t1 + kPStep, k_lds0, v_lds0, sc_lds0) : 0;
+      compute_tile(t1, valid, k_lds1, v_lds1, sc_lds1);
+      __syncthreads();
+      valid = valid_next;
     }
   }
 
-  l = sum_xor32(sum_xor16(l));
-  if (!row_ok) return;
-  const float scale = l > 0.0f ? cs / l : 0.0f;
-  uint16_t* op = a.out + ((int64_t)(q_begin + qi) * a.hq + qh) * kHeadDim;
 #pragma unroll
-  for (int dt = 0; dt < 8; ++dt) {
-    const f32x4 o = acc[dt] * scale;
-    const uint32_t lo = (uint32_t)A::from_f32(o[0]) | ((uint32_t)A::from_f32(o[1]) << 16);
-    const uint32_t hi = (uint32_t)A::from_f32(o[2]) | ((uint32_t)A::from_f32(o[3]) << 16);
-    *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{lo, hi};
+  for (int b = 0; b < kPBlocks; ++b) {
+    const float lt = sum_xor32(sum_xor16(l[b]));
+    if (!row_ok[b]) continue;
+    const float scale = lt > 0.0f && fcur > 0.0f ? 1.0f / (fcur * lt) : 0.0f;
+    uint16_t* op = a.out + ((int64_t)(q_begin + w_q0 + b * a.tpr + n / a.gc) * a.hq + qh[b]) * kHeadDim;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const f32x4 o = acc[b][dt] * scale;
+      const uint32_t lo = (uint32_t)A::from_f32(o[0]) | ((uint32_t)A::from_f32(o[1]) << 16);
+      const uint32_t hi = (uint32_t)A::from_f32(o[2]) | ((uint32_t)A::from_f32(o[3]) << 16);
+      *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{lo, hi};
+    }
   }
 }
 
@@ -346,7 +487,7 @@ extern "C" int mskv_fp8_prefill_attention(
   a.bs = block_size;
   a.w = max_blocks_per_seq;
   a.scale_log2 = softmax_scale * mskv::kLog2e;
-  const int per_wg = mskv::kPWaves * a.tpr;
+  const int per_wg = mskv::kPWaves * mskv::kPBlocks * a.tpr;
   const dim3 grid((unsigned)((max_seqlen_q + per_wg - 1) / per_wg),
                   (unsigned)(num_kv_heads * a.qgroups), (unsigned)num_seqs);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
