@@ -134,10 +134,11 @@ def prefill_flops(seqs, cached, new, hq, d):
     return 4 * d * visits * hq * seqs
 
 
-def time_prefill(dev, iters=20, warmup=3):
+def time_prefill(dev, iters=20, warmup=3, dtype=torch.bfloat16):
     """Varlen chunked prefill: 8 sequences x (8192 cached + 2048 new tokens),
-    32 q / 8 kv heads, bf16 q/k/v N(0,1) with 1% of K entries x20, all
-    10240 tokens of each sequence stored first (as Attention does)."""
+    32 q / 8 kv heads, q/k/v N(0,1) (bf16 by default) with 1% of K entries
+    x20, all 10240 tokens of each sequence stored first (as Attention
+    does)."""
     from microserve_amd import fp8_varlen_prefill_attention, store_fp8_kvcache
     gen = torch.Generator().manual_seed(77)
     lk = PRE_CACHED + PRE_NEW
@@ -148,14 +149,14 @@ def time_prefill(dev, iters=20, warmup=3):
     pos = torch.arange(lk)
     slots = (tables[:, pos // BS].long() * BS + pos % BS).reshape(-1)
     key = torch.randn(slots.numel(), HK, D, generator=gen)
-    key = torch.where(torch.rand(key.shape, generator=gen) < 0.01, key * 20, key).bfloat16()
-    value = torch.randn(slots.numel(), HK, D, generator=gen).bfloat16()
+    key = torch.where(torch.rand(key.shape, generator=gen) < 0.01, key * 20, key).to(dtype)
+    value = torch.randn(slots.numel(), HK, D, generator=gen).to(dtype)
     kc = torch.zeros(pool, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev)
     vc = torch.zeros_like(kc)
     ks = torch.ones(pool, BS, HK, device=dev)
     vs = torch.ones_like(ks)
     store_fp8_kvcache(key.to(dev), value.to(dev), kc, vc, ks, vs, slots.to(dev))
-    q = torch.randn(PRE_SEQS * PRE_NEW, HQ, D, generator=gen).bfloat16().to(dev)
+    q = torch.randn(PRE_SEQS * PRE_NEW, HQ, D, generator=gen).to(dtype).to(dev)
     cu_q = torch.arange(0, PRE_SEQS + 1, dtype=torch.int32, device=dev) * PRE_NEW
     cu_k = torch.arange(0, PRE_SEQS + 1, dtype=torch.int32, device=dev) * lk
     tables = tables.to(dev)
@@ -179,7 +180,7 @@ def time_prefill(dev, iters=20, warmup=3):
     flop = prefill_flops(PRE_SEQS, PRE_CACHED, PRE_NEW, HQ, D)
     tflops = flop / us / 1e6
     return {"workload": "varlen chunked prefill, 8 seqs x (8192 cached + 2048 new), "
-                        "32 q / 8 kv heads, fp8 cache, bf16 q",
+                        f"32 q / 8 kv heads, fp8 cache, {str(dtype).split('.')[-1]} q",
             "us": round(us, 2), "flop": flop, "tflops": round(tflops, 1),
             "peak_tflops": FP8_PEAK_TFLOPS, "frac": round(tflops / FP8_PEAK_TFLOPS, 4)}
 
@@ -221,6 +222,8 @@ def main():
                     help="time decode only (no store fill timing, no CPU baseline)")
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the varlen chunked prefill workload")
+    ap.add_argument("--prefill-dtype", choices=["bf16", "fp16"], default="bf16",
+                    help="activation type of the --prefill-only workload")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run the 1 GiB copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
@@ -233,7 +236,8 @@ def main():
         calibrate_copy(dev)
         return
     if args.prefill_only:
-        print(json.dumps({"prefill": time_prefill(dev)}))
+        dtype = torch.bfloat16 if args.prefill_dtype == "bf16" else torch.float16
+        print(json.dumps({"prefill": time_prefill(dev, dtype=dtype)}))
         return
     from microserve_amd import decode_num_splits, fp8_decode_attention
     w = build_workload(dev)

@@ -43,21 +43,26 @@
 namespace mskv {
 
 constexpr int kPStep = 128;  // keys per tile
-constexpr int kPWaves = 4;
-constexpr int kPBlocks = 2;  // 16-row blocks per wave
-constexpr int kPThreads = 64 * kPWaves;
+// A workgroup covers 128 rows.  bf16 (two query parts) runs 4 waves of two
+// 16-row blocks; fp16 (three parts) needs 24 more registers per block and
+// runs 8 waves of one block, which avoids spills.
+template <int NQ> struct PShape {
+  static constexpr int blocks = NQ == 2 ? 2 : 1;  // 16-row blocks per wave
+  static constexpr int waves = 8 / blocks;
+  static constexpr int threads = 64 * waves;
+};
 // The running max may lag a row's true max by up to kPSlack (log2 units)
-// before the accumulator is rescaled, so p = exp2(x - m) <= 2^kPSlack.  The
-// tile's v_scales are scaled to at most kPVScaleMax, which keeps p * v_scale
-// within e4m3's 448 and puts p = 1 near 100: probabilities down to ~2^-8
-// keep both of their e4m3 parts in the normal range.  (A slack of 2^8 put
-// p = 1 near 1.5 and measured 2.2e-2 max-abs error with 1% x20 K outliers.)
-constexpr float kPSlack = 2.0f;
-constexpr float kPVScaleMax = 96.0f;
+// before the accumulator is rescaled.  P is normalized per row and tile
+// (see below), so the slack does not cost P precision.
+constexpr float kPSlack = 8.0f;
+// The tile's v_scales are scaled by a power of two to at most this value, so
+// p * v_scale (p <= 1 after the per-row normalization) stays within 448.
+constexpr float kPVScaleMax = 384.0f;
 
 // e4m3 parts the query is split into: a bf16 value has 8 significant bits
 template <typename T> struct QuerySplit { static constexpr int parts = 3; };
 template <> struct QuerySplit<__bf16> { static constexpr int parts = 2; };
+template <typename T> using PShapeOf = PShape<QuerySplit<T>::parts>;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -77,8 +82,15 @@ struct PrefillArgs {
 };
 
 __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, f32x4 c) {
-  // scale operands 0 select the unscaled v_mfma_f32_16x16x128_f8f6f4
+  // compile-time zero scales select the unscaled v_mfma_f32_16x16x128_f8f6f4
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
+}
+
+// The same MFMA with an E8M0 block scale on B: lane (g, n)'s scale byte sb
+// multiplies its column n, k-block g by 2^(sb - 127) (A's scale is 1.0).
+__device__ __forceinline__ f32x4 mfma_fp8_scale_b(const i32x8& a, const i32x8& b, f32x4 c,
+                                                  int sb) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, sb);
 }
 
 // largest power of two <= x, for a positive normal x
@@ -98,9 +110,11 @@ __device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, void* lds, u
 }
 
 template <typename T>
-__global__ __launch_bounds__(kPThreads, 2) void prefill_fp8_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(PrefillArgs a) {
   using A = Act<T>;
   constexpr int NQ = QuerySplit<T>::parts;
+  constexpr int kPBlocks = PShapeOf<T>::blocks;
+  constexpr int kPWaves = PShapeOf<T>::waves;
   // two tile buffers as separate objects, and a loop unrolled by two, so
   // the compiler can see that the direct loads into one buffer never alias
   // the reads of the other (otherwise it waits for them before every read)
@@ -207,7 +221,9 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_fp8_kernel(PrefillArgs a
     m[b] = -INFINITY;
     l[b] = 0.0f;
   }
-  float fcur = 0.0f;  // power-of-two scale of p * v_scale in acc (0: none yet)
+  // acc and l are kept in units of fcur, the power-of-two scale applied to
+  // p * v_scale; lf = log2(fcur) is folded into the exp argument
+  float fcur = 1.0f, lf = 0.0f;
 
   // K operand: key n of each 16-key group, 16-byte chunks 2g and 2g + 1;
   // the swizzle of rows 16t + n does not depend on t
@@ -234,9 +250,10 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_fp8_kernel(PrefillArgs a
       reinterpret_cast<uintptr_t>(a.bt));
 
   // Stage tile t0 into LDS buffer `buf` with direct loads; returns the
-  // number of keys holding real tokens.  Wave w's j-th K (and V) load fills
-  // tile rows 8(4j + w) .. +8: lane i lands in slot i of that kilobyte, i.e.
-  // row 8(4j + w) + i/8 at swizzled position i%8, so it reads logical chunk
+  // number of keys holding real tokens.  With W waves, wave w's j-th K (and
+  // V) load fills tile rows 8(Wj + w) .. +8: lane i lands in slot i of that
+  // kilobyte, i.e. row 8(Wj + w) + i/8 at swizzled position i%8, so it reads
+  // logical chunk
   // (i%8) ^ swizzle(row); four consecutive lanes still read one aligned
   // 64-byte half row.  The resources end at the last valid row, so rows past
   // it read as zeros (a stray NaN byte would otherwise poison the MFMA sum)
@@ -255,16 +272,19 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_fp8_kernel(PrefillArgs a
                               valid > 0 ? (uint32_t)(off + valid) * a.hk * 4u : 0u);
     const uint32_t base = (uint32_t)off * rstride + (uint32_t)kvh * kHeadDim;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 8 * (4 * j + wave) + (lane >> 3);
+    for (int j = 0; j < 16 / kPWaves; ++j) {
+      const int row = 8 * (kPWaves * j + wave) + (lane >> 3);
       const int c = (lane & 7) ^ ((row >> 1) & 7);
       const uint32_t o = base + (uint32_t)row * rstride + 16u * c;
-      lds_load16(kr, kt + 1024 * (4 * j + wave), o);
-      lds_load16(vr, vt + 1024 * (4 * j + wave), o);
+      lds_load16(kr, kt + 1024 * (kPWaves * j + wave), o);
+      lds_load16(vr, vt + 1024 * (kPWaves * j + wave), o);
     }
-    const int key = 64 * (wave & 1) + lane;
-    lds_load4(sr, &sct[wave >> 1][64 * (wave & 1)],
-             (((uint32_t)off + key) * a.hk + kvh) * 4u);
+    // waves 0-1 load the k_scales, waves 2-3 the v_scales
+    if (wave < 4) {
+      const int key = 64 * (wave & 1) + lane;
+      lds_load4(sr, &sct[wave >> 1][64 * (wave & 1)],
+                (((uint32_t)off + key) * a.hk + kvh) * 4u);
+    }
     return valid;
   };
 
@@ -344,39 +364,67 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_fp8_kernel(PrefillArgs a
       if (vm > 0.0f) {
         const float ft = pow2_floor(kPVScaleMax / vm);
         if (ft != fcur) {
-          if (fcur > 0.0f) {
-            const float r = ft / fcur;  // a power of two: exact
+          const float r = ft / fcur;  // a power of two: exact
 #pragma unroll
-            for (int b = 0; b < kPBlocks; ++b)
+          for (int b = 0; b < kPBlocks; ++b) {
+            l[b] *= r;
 #pragma unroll
-              for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= r;
+            for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= r;
           }
           fcur = ft;
+          lf = (float)((int)((__float_as_uint(ft) >> 23) & 0xFFu) - 127);
         }
       }
-      // P8 = e4m3 hi + lo of p * v_scale * fcur, p = exp2(x * qs - m)
+      // P, normalized per row and tile: with k = floor(m - tile max) the row's
+      // largest p * 2^k is at most 1, so a tile far below the row max keeps
+      // its probabilities out of e4m3's underflow; the PV MFMA multiplies
+      // 2^-k back through its per-row E8M0 scale on P.
+      // y = p * 2^k * fcur * v_scale is split into e4m3 hi + lo.  l sums the
+      // weights the MFMA actually applies, (hi + lo) / v_scale * 2^-k, not p:
+      // the output is then an exact convex combination of V rows under those
+      // weights, so a row dominated by one key returns that key's V without
+      // the split's 2^-9 error.
       i32x8 p8h[kPBlocks], p8l[kPBlocks];
+      float m_use[kPBlocks], lsum[kPBlocks];
+      int kr[kPBlocks];
 #pragma unroll
       for (int b = 0; b < kPBlocks; ++b) {
-        const float m_use = m[b] == -INFINITY ? 0.0f : m[b];
-        float psum = 0.0f;
+        const float kf =
+            tm[b] == -INFINITY ? 0.0f : fminf(floorf(m[b] - tm[b]), 127.0f);
+        kr[b] = (int)kf;
+        m_use[b] = (m[b] == -INFINITY ? 0.0f : m[b]) - lf - kf;
+        lsum[b] = 0.0f;
+      }
+      typedef float f32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-        for (int tt = 0; tt < 8; ++tt) {
-          const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g) * fcur;
+      for (int tt = 0; tt < 8; ++tt) {
+        const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
+        f32x4 rv;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) rv[r] = vsc[r] > 0.0f ? __builtin_amdgcn_rcpf(vsc[r]) : 0.0f;
+#pragma unroll
+        for (int b = 0; b < kPBlocks; ++b) {
           float y[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float p = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use));
-            psum += p;
-            y[r] = p * vsc[r];
-          }
-          uint32_t h, lo;
-          split_fp8x4(y[0], y[1], y[2], y[3], h, lo);
+          for (int r = 0; r < 4; ++r)
+            y[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b])) * vsc[r];
+          const uint32_t h = pack_fp8x4(y[0], y[1], y[2], y[3]);
+          const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
+          const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
+          const uint32_t lo = pack_fp8x4(y[0] - h01[0], y[1] - h01[1], y[2] - h23[0],
+                                         y[3] - h23[1]);
+          const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
+          const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+          lsum[b] = fmaf(h01[0] + l01[0], rv[0], lsum[b]);
+          lsum[b] = fmaf(h01[1] + l01[1], rv[1], lsum[b]);
+          lsum[b] = fmaf(h23[0] + l23[0], rv[2], lsum[b]);
+          lsum[b] = fmaf(h23[1] + l23[1], rv[3], lsum[b]);
           p8h[b][tt] = (int)h;
           p8l[b][tt] = (int)lo;
         }
-        l[b] += psum;
       }
+#pragma unroll
+      for (int b = 0; b < kPBlocks; ++b) l[b] += __builtin_amdgcn_ldexpf(lsum[b], -kr[b]);
       // O^T += V^T . P8^T, one 16-wide d tile per MFMA pair
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
@@ -392,8 +440,8 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_fp8_kernel(PrefillArgs a
         }
 #pragma unroll
         for (int b = 0; b < kPBlocks; ++b) {
-          acc[b][dt] = mfma_fp8(va, p8h[b], acc[b][dt]);
-          acc[b][dt] = mfma_fp8(va, p8l[b], acc[b][dt]);
+          acc[b][dt] = mfma_fp8_scale_b(va, p8h[b], acc[b][dt], 127 - kr[b]);
+          acc[b][dt] = mfma_fp8_scale_b(va, p8l[b], acc[b][dt], 127 - kr[b]);
         }
       }
     }
@@ -424,7 +472,7 @@ __global__ __launch_bounds__(kPThreads, 2) void prefill_fp8_kernel(PrefillArgs a
   for (int b = 0; b < kPBlocks; ++b) {
     const float lt = sum_xor32(sum_xor16(l[b]));
     if (!row_ok[b]) continue;
-    const float scale = lt > 0.0f && fcur > 0.0f ? 1.0f / (fcur * lt) : 0.0f;
+    const float scale = lt > 0.0f ? 1.0f / lt : 0.0f;
     uint16_t* op = a.out + ((int64_t)(q_begin + w_q0 + b * a.tpr + n / a.gc) * a.hq + qh[b]) * kHeadDim;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
@@ -487,13 +535,15 @@ extern "C" int mskv_fp8_prefill_attention(
   a.bs = block_size;
   a.w = max_blocks_per_seq;
   a.scale_log2 = softmax_scale * mskv::kLog2e;
-  const int per_wg = mskv::kPWaves * mskv::kPBlocks * a.tpr;
+  const int per_wg = 8 * a.tpr;  // 128 rows: 8 blocks of 16 rows
   const dim3 grid((unsigned)((max_seqlen_q + per_wg - 1) / per_wg),
                   (unsigned)(num_kv_heads * a.qgroups), (unsigned)num_seqs);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (act_dtype == MSKV_BFLOAT16)
-    hipLaunchKernelGGL(mskv::prefill_fp8_kernel<__bf16>, grid, dim3(mskv::kPThreads), 0, s, a);
+    hipLaunchKernelGGL(mskv::prefill_fp8_kernel<__bf16>, grid,
+                       dim3(mskv::PShapeOf<__bf16>::threads), 0, s, a);
   else
-    hipLaunchKernelGGL(mskv::prefill_fp8_kernel<_Float16>, grid, dim3(mskv::kPThreads), 0, s, a);
+    hipLaunchKernelGGL(mskv::prefill_fp8_kernel<_Float16>, grid,
+                       dim3(mskv::PShapeOf<_Float16>::threads), 0, s, a);
   return (int)hipGetLastError();
 }
