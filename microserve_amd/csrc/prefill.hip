@@ -332,10 +332,10 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
       float tm[kPBlocks];
 #pragma unroll
       for (int b = 0; b < kPBlocks; ++b) {
-        float v = -INFINITY;
+        float v = fmaxf(fmaxf(st[b][0][0], st[b][0][1]), fmaxf(st[b][0][2], st[b][0][3]));
 #pragma unroll
-        for (int tt = 0; tt < 8; ++tt)
-          v = fmaxf(v, fmaxf(fmaxf(st[b][tt][0], st[b][tt][1]), fmaxf(st[b][tt][2], st[b][tt][3])));
+        for (int tt = 1; tt < 8; ++tt)
+          v = fmaxf(fmaxf(v, st[b][tt][0]), fmaxf(fmaxf(st[b][tt][1], st[b][tt][2]), st[b][tt][3]));
         tm[b] = max_xor32(max_xor16(v)) * qs[b];
       }
       bool grow = false;
@@ -399,9 +399,11 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
 #pragma unroll
       for (int tt = 0; tt < 8; ++tt) {
         const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
+        // v_scale is 0 only for keys past `valid`, whose weights are 0
         f32x4 rv;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) rv[r] = vsc[r] > 0.0f ? __builtin_amdgcn_rcpf(vsc[r]) : 0.0f;
+        for (int r = 0; r < 4; ++r)
+          rv[r] = full || vsc[r] > 0.0f ? __builtin_amdgcn_rcpf(vsc[r]) : 0.0f;
 #pragma unroll
         for (int b = 0; b < kPBlocks; ++b) {
           float y[4];
