@@ -185,6 +185,45 @@ def time_prefill(dev, iters=20, warmup=3, dtype=torch.bfloat16):
             "peak_tflops": FP8_PEAK_TFLOPS, "frac": round(tflops / FP8_PEAK_TFLOPS, 4)}
 
 
+FRESH_SEQS, FRESH_LEN = 8, 8192
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def time_fresh_prefill(dev, iters=10, warmup=2):
+    """Fresh PREFILL (unquantized q/k/v, causal, the flash_attn_varlen_func
+    call of the FP8 path): 8 sequences x 8192 new tokens, 32 q / 8 kv heads,
+    bf16 N(0,1)."""
+    from microserve_amd import varlen_attention
+    gen = torch.Generator().manual_seed(88)
+    n = FRESH_SEQS * FRESH_LEN
+    q = torch.randn(n, HQ, D, generator=gen).bfloat16().to(dev)
+    k = torch.randn(n, HK, D, generator=gen).bfloat16().to(dev)
+    v = torch.randn(n, HK, D, generator=gen).bfloat16().to(dev)
+    cu = torch.arange(0, FRESH_SEQS + 1, dtype=torch.int32, device=dev) * FRESH_LEN
+
+    def run():
+        return varlen_attention(q, k, v, cu, cu, FRESH_LEN, FRESH_LEN, D ** -0.5)
+
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
+    for e0, e1 in evs:
+        e0.record(stream)
+        run()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    us = sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
+    flop = prefill_flops(FRESH_SEQS, 0, FRESH_LEN, HQ, D)
+    tflops = flop / us / 1e6
+    return {"workload": "fresh causal prefill, 8 seqs x 8192 tokens, 32 q / 8 kv heads, "
+                        "bf16 q/k/v (16-bit MFMA)",
+            "us": round(us, 2), "flop": flop, "tflops": round(tflops, 1),
+            "peak_tflops": BF16_PEAK_TFLOPS, "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
+
+
 def calibrate_copy(dev, nbytes=1 << 30, iters=5):
     """A plain device copy of known size, for scaling the FETCH_SIZE and
     WRITE_SIZE counters to bytes (run it under rocprofv3 --pmc)."""
@@ -224,6 +263,8 @@ def main():
                     help="time only the varlen chunked prefill workload")
     ap.add_argument("--prefill-dtype", choices=["bf16", "fp16"], default="bf16",
                     help="activation type of the --prefill-only workload")
+    ap.add_argument("--fresh-only", action="store_true",
+                    help="time only the fresh (unquantized) prefill workload")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run the 1 GiB copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
@@ -234,6 +275,9 @@ def main():
     dev = "cuda:0"
     if args.calibrate_copy:
         calibrate_copy(dev)
+        return
+    if args.fresh_only:
+        print(json.dumps({"fresh_prefill": time_fresh_prefill(dev)}))
         return
     if args.prefill_only:
         dtype = torch.bfloat16 if args.prefill_dtype == "bf16" else torch.float16
@@ -307,6 +351,7 @@ def main():
                            for k, v in store.items()}
     if not args.decode_only:
         result["prefill"] = time_prefill(dev)
+        result["fresh_prefill"] = time_fresh_prefill(dev)
     if not args.no_cpu and not args.decode_only:
         result["cpu_baseline"] = cpu_baseline(w)
     print(json.dumps(result), flush=True)

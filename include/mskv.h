@@ -122,8 +122,9 @@ int mskv_fp8_decode_attention(const void* query, const void* k_cache,
  * p < (Lk - Lq) + i + 1 (fp8_chunk_prefill_attention.py:52-54).
  * When cu_seqlens_q and cu_seqlens_k are both NULL the batch is one
  * sequence of total_q queries over prefix_len + total_q positions, exactly
- * the reference's signature.  QK^T and PV run as FP8 MFMA contractions with
- * a per-row fp32 scale on the query and on the probabilities.
+ * the reference's signature.  QK^T and PV run as FP8 MFMA contractions: the
+ * query is split into e4m3 parts under a power-of-two row scale, and the
+ * probabilities into hi + lo parts under a per-row E8M0 block scale.
  * query/out: [total_q, num_q_heads, head_dim] in act_dtype; block_tables:
  * int32 [num_seqs, max_blocks_per_seq].
  * Supported: head_dim == 128, block_size % 128 == 0, GQA group <= 16 or a
@@ -141,6 +142,30 @@ int mskv_fp8_prefill_attention(const void* query, const void* k_cache,
                                int64_t num_blocks, int max_blocks_per_seq,
                                float softmax_scale, int act_dtype,
                                void* stream);
+
+/*
+ * Causal varlen attention over unquantized q/k/v: the fresh PREFILL of the
+ * FP8-KV path.
+ *
+ * Replaces flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k,
+ * max_seqlen_q, max_seqlen_k, softmax_scale, causal=True), called by
+ * microserve/layers/attention.py:49-55 on the step's new tokens.  Sequence
+ * s owns query rows [cu_seqlens_q[s], cu_seqlens_q[s+1]) and key rows
+ * [cu_seqlens_k[s], cu_seqlens_k[s+1]); query i sees key j iff
+ * j <= i + Lk - Lq (flash-attn's bottom-right causal alignment); a row that
+ * sees no key is zero.  QK^T and PV run on 16-bit MFMA in act_dtype with
+ * fp32 accumulation; the probabilities are rounded to act_dtype.
+ * query/out: [total_q, num_q_heads, head_dim]; key/value:
+ * [total_k, num_kv_heads, head_dim], all contiguous in act_dtype.
+ * Supported: head_dim == 128, GQA group <= 16 or a multiple of 16.
+ */
+int mskv_prefill_attention(const void* query, const void* key,
+                           const void* value, void* out,
+                           const int32_t* cu_seqlens_q,
+                           const int32_t* cu_seqlens_k, int num_seqs,
+                           int64_t total_q, int64_t total_k, int max_seqlen_q,
+                           int num_q_heads, int num_kv_heads, int head_dim,
+                           float softmax_scale, int act_dtype, void* stream);
 
 #ifdef __cplusplus
 }

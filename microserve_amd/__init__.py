@@ -1,7 +1,8 @@
 """MI355X-native FP8 paged-KV hot path of microserve.
 
 Drop-in replacements for ``microserve.layers.fp8_kv_cache``,
-``fp8_decode_attention``, ``fp8_chunk_prefill_attention``,
+``fp8_decode_attention``, ``fp8_chunk_prefill_attention``, the fresh-prefill
+``flash_attn_varlen_func`` call,
 ``layers.attention.Attention`` (FP8 branch) and ``utils.context``, backed by
 hand-written gfx950 HIP kernels behind the C ABI in ``include/mskv.h``.
 """
@@ -13,4 +14,6 @@ from microserve_amd.fp8_decode_attention import (  # noqa: F401
     decode_num_splits, fp8_decode_attention)
 from microserve_amd.fp8_chunk_prefill_attention import (  # noqa: F401
     fp8_chunk_prefill_attention, fp8_varlen_prefill_attention)
+from microserve_amd.varlen_attention import (  # noqa: F401
+    flash_attn_varlen_func, varlen_attention)
 from microserve_amd.attention import Attention  # noqa: F401

@@ -39,6 +39,9 @@ _PROTOS = {
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
         _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,
         _c_int, _c_f32, _c_int, _vp]),
+    "mskv_prefill_attention": (_c_int, [
+        _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _c_int,
+        _c_int, _c_int, _c_int, _c_f32, _c_int, _vp]),
 }
 
 EXPORTED = tuple(_PROTOS)

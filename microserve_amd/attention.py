@@ -14,12 +14,10 @@ import torch
 from torch import nn
 
 from microserve_amd.context import AttentionMode, get_context
-from microserve_amd.fp8_chunk_prefill_attention import (
-    fp8_chunk_prefill_attention,
-    fp8_varlen_prefill_attention,
-)
+from microserve_amd.fp8_chunk_prefill_attention import fp8_chunk_prefill_attention
 from microserve_amd.fp8_decode_attention import fp8_decode_attention
 from microserve_amd.fp8_kv_cache import store_fp8_kvcache
+from microserve_amd.varlen_attention import varlen_attention
 
 
 class Attention(nn.Module):
@@ -52,17 +50,12 @@ class Attention(nn.Module):
                 q, k_cache, v_cache, self.k_scale_cache, self.v_scale_cache,
                 ctx.cache_seqlens, ctx.block_tables, self.scale)
         if ctx.mode is AttentionMode.PREFILL:
-            # The reference runs flash_attn_varlen_func on the unquantized
-            # q/k/v here (attention.py:49-55).  This library attends over the
-            # just-stored FP8 cache instead, which needs the block tables.
-            if ctx.block_tables is None:
-                raise NotImplementedError(
-                    "fresh PREFILL needs ctx.block_tables: attention runs over "
-                    "the stored FP8 cache")
-            return fp8_varlen_prefill_attention(
-                q, k_cache, v_cache, self.k_scale_cache, self.v_scale_cache,
-                ctx.block_tables, ctx.cu_seqlens_q, ctx.cu_seqlens_k,
-                ctx.max_seqlen_q, self.scale)
+            # fresh prefill attends over the unquantized new tokens, as the
+            # reference's flash_attn_varlen_func call does (attention.py:49-55)
+            return varlen_attention(
+                q, k, v, cu_seqlens_q=ctx.cu_seqlens_q,
+                cu_seqlens_k=ctx.cu_seqlens_k, max_seqlen_q=ctx.max_seqlen_q,
+                max_seqlen_k=ctx.max_seqlen_k, softmax_scale=self.scale, causal=True)
         if ctx.mode is AttentionMode.CHUNK_PREFILL:
             return fp8_chunk_prefill_attention(
                 q, k_cache, v_cache, self.k_scale_cache, self.v_scale_cache,

@@ -35,6 +35,13 @@ How each function is pinned (the checks live in ``tests/test_oracle.py``):
   rows, and by invariants: block relabelling, ``seq_len == 0 -> 0``, a
   one-token context returns that token's dequantized V, equal scores return
   the mean of V.
+* ``dense_varlen_attention`` -- the fresh PREFILL over unquantized q/k/v
+  (flash-attn's causal convention, bottom-right aligned).  Pinned against
+  ``dense_varlen_attention_loop`` (float64 per-query softmax), against
+  ``scaled_dot_product_attention(is_causal=True)`` where ``Lq == Lk``, and
+  against ``varlen_prefill_attention`` on a cache that holds the same K/V
+  exactly (e4m3-representable rows with unit scale), which ties the two
+  causal conventions together.
 * ``chunk_prefill_attention`` / ``varlen_prefill_attention`` -- pinned
   against ``varlen_prefill_attention_loop`` (per-query direct softmax in
   float64, causal ``visible = prefix + i + 1`` from
@@ -310,6 +317,80 @@ def chunk_prefill_attention(query, k_cache, v_cache, k_scale_cache,
     return varlen_prefill_attention(q, k_cache, v_cache, k_scale_cache,
                                     v_scale_cache, table, cu_q, cu_k,
                                     softmax_scale)
+
+
+def dense_varlen_attention(query, key, value, cu_seqlens_q, cu_seqlens_k,
+                           softmax_scale) -> torch.Tensor:
+    """Causal varlen attention over unquantized q/k/v, float32: the fresh
+    PREFILL of the FP8 path, which the reference runs as
+    ``flash_attn_varlen_func(q, k, v, ..., causal=True)`` on the new tokens
+    (``attention.py:49-55``).
+
+    ``key``/``value`` are ``[total_k, H_kv, D]``; sequence ``s`` owns query
+    rows ``cu_q[s]..cu_q[s+1]`` and key rows ``cu_k[s]..cu_k[s+1]``.  The
+    causal mask is flash-attn's bottom-right alignment: query ``i`` sees key
+    ``j`` iff ``j <= i + Lk - Lq`` (the same bound as the paged prefill's
+    ``prefix + i + 1`` with ``prefix = Lk - Lq``).  Rows that see no key are
+    zero.  Returns float32 ``[total_q, H_q, D]``.
+    """
+    q = _as_t(query).float()
+    k_all = _as_t(key).float()
+    v_all = _as_t(value).float()
+    tq, hq, d = q.shape
+    hk = k_all.shape[1]
+    group = hq // hk
+    cu_q = [int(x) for x in _as_t(cu_seqlens_q).reshape(-1).tolist()]
+    cu_k = [int(x) for x in _as_t(cu_seqlens_k).reshape(-1).tolist()]
+    out = torch.zeros(tq, hq, d, dtype=torch.float32)
+    for s in range(len(cu_q) - 1):
+        lq = cu_q[s + 1] - cu_q[s]
+        lk = cu_k[s + 1] - cu_k[s]
+        if lq <= 0 or lk <= 0:
+            continue
+        k = k_all[cu_k[s]:cu_k[s + 1]]
+        v = v_all[cu_k[s]:cu_k[s + 1]]
+        qs = q[cu_q[s]:cu_q[s + 1]].view(lq, hk, group, d)
+        scores = torch.einsum("ikgd,lkd->kgil", qs, k) * softmax_scale
+        visible = torch.arange(lk)[None, :] <= (torch.arange(lq) + lk - lq)[:, None]
+        scores = scores.masked_fill(~visible[None, None], float("-inf"))
+        p = torch.nan_to_num(scores.softmax(-1), nan=0.0)  # rows that see nothing
+        o = torch.einsum("kgil,lkd->ikgd", p, v)
+        out[cu_q[s]:cu_q[s + 1]] = o.reshape(lq, hq, d)
+    return out
+
+
+def dense_varlen_attention_loop(query, key, value, cu_seqlens_q, cu_seqlens_k,
+                                softmax_scale) -> np.ndarray:
+    """Per-query direct softmax in float64 over unquantized q/k/v (tiny
+    inputs only); shares no code with ``dense_varlen_attention``."""
+    q = np.asarray(_as_t(query).float().numpy(), dtype=np.float64)
+    k = np.asarray(_as_t(key).float().numpy(), dtype=np.float64)
+    v = np.asarray(_as_t(value).float().numpy(), dtype=np.float64)
+    cu_q = np.asarray(_as_t(cu_seqlens_q).numpy()).reshape(-1)
+    cu_k = np.asarray(_as_t(cu_seqlens_k).numpy()).reshape(-1)
+    tq, hq, d = q.shape
+    hk = k.shape[1]
+    group = hq // hk
+    out = np.zeros((tq, hq, d))
+    for s in range(len(cu_q) - 1):
+        lq = int(cu_q[s + 1] - cu_q[s])
+        lk = int(cu_k[s + 1] - cu_k[s])
+        for i in range(lq):
+            last = i + lk - lq  # keys 0..last are visible
+            if last < 0:
+                continue
+            for h in range(hq):
+                kv = h // group
+                sc = [float(np.dot(q[cu_q[s] + i, h], k[cu_k[s] + j, kv])) * softmax_scale
+                      for j in range(last + 1)]
+                mx = max(sc)
+                w = [np.exp(x - mx) for x in sc]
+                tot = sum(w)
+                acc = np.zeros(d)
+                for j, wj in enumerate(w):
+                    acc += wj * v[cu_k[s] + j, kv]
+                out[cu_q[s] + i, h] = acc / tot
+    return out
 
 
 def varlen_prefill_attention_loop(query, k_cache, v_cache, k_scale_cache,

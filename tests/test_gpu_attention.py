@@ -72,7 +72,10 @@ def test_attention_chunk_then_decode():
     H.assert_attention_close(out, ref)
 
 
-def test_attention_fresh_prefill_over_stored_cache():
+def test_attention_fresh_prefill_attends_unquantized_and_stores():
+    """PREFILL as the reference runner issues it (no block tables): the K/V
+    are stored into the FP8 cache and attention runs over the unquantized
+    new tokens (flash_attn_varlen_func, attention.py:49-55)."""
     gen = torch.Generator().manual_seed(311)
     attn = _layer(nb=8)
     lens = [100, 37]
@@ -83,14 +86,22 @@ def test_attention_fresh_prefill_over_stored_cache():
     cu = torch.tensor([0, 100, 137], dtype=torch.int32)
     set_context(Context(mode=AttentionMode.PREFILL, cu_seqlens_q=cu.to(H.DEV),
                         cu_seqlens_k=cu.to(H.DEV), max_seqlen_q=100, max_seqlen_k=100,
-                        slot_mapping=slots.to(H.DEV), block_tables=tables.to(H.DEV)))
+                        slot_mapping=slots.to(H.DEV)))
     try:
         out = attn(q.to(H.DEV), k.to(H.DEV), v.to(H.DEV))
     finally:
         reset_context()
-    kc, vc, ks, vs = _np_caches(attn)
-    ref = O.varlen_prefill_attention(q, kc, vc, ks, vs, tables, cu, cu, H.D ** -0.5)
+    ref = O.dense_varlen_attention(q, k, v, cu, cu, H.D ** -0.5)
     H.assert_attention_close(out, ref)
+    # the step's K/V were stored: chunk prefill over the cache agrees with
+    # the FP8-dequantized oracle
+    kc, vc, ks, vs = _np_caches(attn)
+    ref_cache = O.varlen_prefill_attention(q, kc, vc, ks, vs, tables, cu, cu, H.D ** -0.5)
+    from microserve_amd import fp8_varlen_prefill_attention
+    got = fp8_varlen_prefill_attention(q.to(H.DEV), attn.k_cache, attn.v_cache, attn.k_scale_cache,
+                                       attn.v_scale_cache, tables.to(H.DEV), cu.to(H.DEV),
+                                       cu.to(H.DEV), 100, H.D ** -0.5)
+    H.assert_attention_close(got, ref_cache)
 
 
 def test_attention_unknown_mode_raises():

@@ -270,6 +270,57 @@ def test_varlen_prefill_vs_loop_and_sdpa():
     assert np.abs(a[0] - dec[0].numpy()).max() < 1e-5
 
 
+def test_dense_varlen_vs_loop_sdpa_and_paged_oracle():
+    """The fresh-PREFILL oracle: float64 loop, SDPA on the square causal
+    case, and the paged oracle on a cache holding the same K/V exactly."""
+    rng = np.random.default_rng(16)
+    hq, hk, d = 4, 2, 32
+    lq = [7, 5, 6]
+    lk = [7, 12, 3]                       # fresh, cached prefix, Lq > Lk
+    cu_q = np.array([0, 7, 12, 18], np.int32)
+    cu_k = np.array([0, 7, 19, 22], np.int32)
+    q = rng.standard_normal((18, hq, d)).astype(np.float32)
+    k = rng.standard_normal((22, hk, d)).astype(np.float32)
+    v = rng.standard_normal((22, hk, d)).astype(np.float32)
+    sc = d ** -0.5
+    a = O.dense_varlen_attention(q, k, v, cu_q, cu_k, sc).numpy()
+    b = O.dense_varlen_attention_loop(q, k, v, cu_q, cu_k, sc)
+    assert np.abs(a - b).max() < 1e-5
+    # Lq > Lk: query i sees keys j <= i - 3; the first three rows see nothing
+    assert np.all(a[12:15] == 0) and np.abs(a[15:18]).max() > 0
+    # square causal == SDPA is_causal (GQA expanded)
+    qq = torch.from_numpy(q[0:7]).permute(1, 0, 2)[None]
+    kk = torch.from_numpy(k[0:7]).permute(1, 0, 2).repeat_interleave(2, 0)[None]
+    vv = torch.from_numpy(v[0:7]).permute(1, 0, 2).repeat_interleave(2, 0)[None]
+    ref = torch.nn.functional.scaled_dot_product_attention(qq, kk, vv, is_causal=True, scale=sc)
+    assert np.abs(a[0:7] - ref[0].permute(1, 0, 2).numpy()).max() < 1e-5
+    # the paged oracle on an exact cache: e4m3-representable rows whose amax is
+    # 448 quantize with scale 1, so the cache holds K/V exactly
+    codes = np.arange(0, 0x7F, dtype=np.uint8)
+    exact = O.e4m3fn_decode(np.concatenate([codes, codes | 0x80]))
+    kx = rng.choice(exact, (22, hk, d)).astype(np.float32)
+    vx = rng.choice(exact, (22, hk, d)).astype(np.float32)
+    kx[:, :, 0] = 448.0
+    vx[:, :, 0] = 448.0
+    bs = 8
+    tables = np.array([[0, -1], [1, 2], [3, -1]], np.int32)
+    kc = np.zeros((4, bs, hk, d), np.uint8)
+    vc = np.zeros_like(kc)
+    ks = np.zeros((4, bs, hk), np.float32)
+    vs = np.zeros_like(ks)
+    slots = np.concatenate([tables[s_][np.arange(n) // bs] * bs + np.arange(n) % bs
+                            for s_, n in enumerate(lk)])
+    O.store_fp8_kvcache(kx, vx, kc, vc, ks, vs, slots)
+    used = np.zeros((4, bs), bool)
+    used.reshape(-1)[slots] = True
+    assert np.all(ks[used] == 1) and np.all(vs[used] == 1)
+    qx = (q * 0.01).astype(np.float32)
+    a = O.dense_varlen_attention(qx, kx, vx, cu_q, cu_k, sc)
+    b = O.varlen_prefill_attention(qx, kc, vc, ks, vs, tables, cu_q, cu_k, sc)
+    ok = [*range(0, 12), *range(15, 18)]           # rows that see at least one key
+    assert torch.allclose(a[ok], b[ok], atol=1e-3, rtol=1e-5)
+
+
 def test_chunk_prefill_wrapper_equals_varlen():
     rng = np.random.default_rng(7)
     bs, hq, hk, d = 16, 4, 2, 32
