@@ -185,6 +185,122 @@ def time_prefill(dev, iters=20, warmup=3, dtype=torch.bfloat16):
             "peak_tflops": FP8_PEAK_TFLOPS, "frac": round(tflops / FP8_PEAK_TFLOPS, 4)}
 
 
+def _time_steps(step, iters, warmup):
+    """Average HIP-event time of step(i) on the current stream, in us."""
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(iters)]
+    for i, (e0, e1) in enumerate(evs):
+        e0.record(stream)
+        step(i)
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
+
+
+def _fill_pages(dev, kc, vc, ks, vs, pages, gen, chunk_pages=512):
+    """store_fp8_kvcache every token of the given pages from bf16 N(0,1)
+    drawn on the device."""
+    from microserve_amd import store_fp8_kvcache
+    bs, hk, d = kc.shape[1], kc.shape[2], kc.shape[3]
+    dgen = torch.Generator(device=dev).manual_seed(int(torch.randint(1 << 30, (1,), generator=gen)))
+    for i in range(0, pages.numel(), chunk_pages):
+        pg = pages[i:i + chunk_pages].to(dev).long()
+        slots = (pg[:, None] * bs + torch.arange(bs, device=dev)[None]).reshape(-1)
+        key = torch.randn(slots.numel(), hk, d, generator=dgen, device=dev, dtype=torch.bfloat16)
+        value = torch.randn(slots.numel(), hk, d, generator=dgen, device=dev, dtype=torch.bfloat16)
+        store_fp8_kvcache(key, value, kc, vc, ks, vs, slots)
+
+
+def time_ragged(dev, iters=50, warmup=5):
+    """Ragged decode stress at the Qwen3-8B shape: batch 256, context lengths
+    log-uniform in [16, 32768], each sequence's blocks sampled without
+    replacement from a 40,000-block pool; one step is the one-token
+    store_kvcache append of every sequence followed by the decode."""
+    from microserve_amd import fp8_decode_attention, store_fp8_kvcache
+    gen = torch.Generator().manual_seed(3)
+    b, pool = 256, 40000
+    lens = torch.exp(torch.empty(b).uniform_(float(torch.log(torch.tensor(16.0))),
+                                             float(torch.log(torch.tensor(32768.0))),
+                                             generator=gen)).long()
+    pages = (lens + BS - 1) // BS
+    width = int(pages.max())
+    perm = torch.randperm(pool, generator=gen)
+    tables = torch.full((b, width), -1, dtype=torch.int32)
+    at = 0
+    for i in range(b):
+        tables[i, :pages[i]] = perm[at:at + pages[i]].to(torch.int32)
+        at += int(pages[i])
+    kc = torch.zeros(pool, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(pool, BS, HK, device=dev)
+    vs = torch.ones_like(ks)
+    _fill_pages(dev, kc, vc, ks, vs, perm[:at], gen)
+    tables_d = tables.to(dev)
+    seqlens = lens.to(torch.int32).to(dev)
+    # the appended token of each sequence is its last position
+    last = (lens - 1)
+    slots = (tables[torch.arange(b), last // BS].long() * BS + last % BS).to(dev)
+    knew = torch.randn(b, HK, D, generator=gen).bfloat16().to(dev)
+    vnew = torch.randn(b, HK, D, generator=gen).bfloat16().to(dev)
+    q = torch.randn(b, HQ, D, generator=gen).bfloat16().to(dev)
+    out = torch.empty_like(q)
+
+    def step(i):
+        store_fp8_kvcache(knew, vnew, kc, vc, ks, vs, slots)
+        fp8_decode_attention(q, kc, vc, ks, vs, seqlens, tables_d, D ** -0.5, out=out)
+
+    us = _time_steps(step, iters, warmup)
+    nbytes = decode_bytes_ragged(lens, HQ, HK, D) + store_bytes(b, HK, D)
+    return {"workload": "ragged decode, batch 256, context log-uniform [16, 32768], "
+                        "40k-block fragmented pool, with the one-token append store",
+            "tokens": int(lens.sum()), "us": round(us, 2), "bytes": nbytes,
+            "gbs": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def decode_bytes_ragged(lens, hq, hk, d, act_bytes=2):
+    kv = int(lens.sum()) * (2 * hk * d + 2 * hk * 4)
+    qo = len(lens) * hq * d * act_bytes * 2
+    tables = 4 * (int(((lens + BS - 1) // BS).sum()) + len(lens))
+    return kv + qo + tables
+
+
+def time_long_context(dev, batch, iters=50, warmup=5):
+    """Long-context decode at the Qwen3-32B shape: 64 q / 8 kv heads, every
+    sequence at context 131072 (512 blocks); two disjoint block sets
+    alternate between steps so the MALL cannot serve the reads."""
+    from microserve_amd import decode_num_splits, fp8_decode_attention
+    gen = torch.Generator().manual_seed(5 + batch)
+    hq, ctx = 64, 131072
+    pages = ctx // BS
+    pool = 2 * batch * pages
+    perm = torch.randperm(pool, generator=gen).to(torch.int32)
+    kc = torch.zeros(pool, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(pool, BS, HK, device=dev)
+    vs = torch.ones_like(ks)
+    _fill_pages(dev, kc, vc, ks, vs, perm, gen)
+    tabs = [perm[:batch * pages].view(batch, pages).contiguous().to(dev),
+            perm[batch * pages:].view(batch, pages).contiguous().to(dev)]
+    seqlens = torch.full((batch,), ctx, dtype=torch.int32, device=dev)
+    q = torch.randn(batch, hq, D, generator=gen).bfloat16().to(dev)
+    out = torch.empty_like(q)
+
+    def step(i):
+        fp8_decode_attention(q, kc, vc, ks, vs, seqlens, tabs[i % 2], D ** -0.5, out=out)
+
+    us = _time_steps(step, iters, warmup)
+    nbytes = decode_bytes(batch, ctx, hq, HK, D)
+    return {"workload": f"Qwen3-32B long-context decode, batch {batch} x context 131072",
+            "splits": decode_num_splits(batch, hq, HK, pages, BS),
+            "us": round(us, 2), "bytes": nbytes, "gbs": round(nbytes / us / 1e3, 1),
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+
 FRESH_SEQS, FRESH_LEN = 8, 8192
 BF16_PEAK_TFLOPS = 2500.0
 
@@ -265,6 +381,8 @@ def main():
                     help="activation type of the --prefill-only workload")
     ap.add_argument("--fresh-only", action="store_true",
                     help="time only the fresh (unquantized) prefill workload")
+    ap.add_argument("--shapes-only", action="store_true",
+                    help="time only the ragged and long-context decode workloads")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run the 1 GiB copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
@@ -275,6 +393,10 @@ def main():
     dev = "cuda:0"
     if args.calibrate_copy:
         calibrate_copy(dev)
+        return
+    if args.shapes_only:
+        print(json.dumps({"ragged": time_ragged(dev),
+                          "long_context": [time_long_context(dev, b) for b in (1, 4)]}))
         return
     if args.fresh_only:
         print(json.dumps({"fresh_prefill": time_fresh_prefill(dev)}))
@@ -349,11 +471,15 @@ def main():
     if store is not None:
         result["store"] = {k: (round(v, 4) if isinstance(v, float) else v)
                            for k, v in store.items()}
+    if not args.no_cpu and not args.decode_only:
+        result["cpu_baseline"] = cpu_baseline(w)
     if not args.decode_only:
         result["prefill"] = time_prefill(dev)
         result["fresh_prefill"] = time_fresh_prefill(dev)
-    if not args.no_cpu and not args.decode_only:
-        result["cpu_baseline"] = cpu_baseline(w)
+        del w
+        torch.cuda.empty_cache()
+        result["ragged"] = time_ragged(dev)
+        result["long_context"] = [time_long_context(dev, b) for b in (1, 4)]
     print(json.dumps(result), flush=True)
 
 

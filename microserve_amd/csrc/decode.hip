@@ -359,6 +359,70 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(
   *reinterpret_cast<uint32_t*>(out + (int64_t)row * kHeadDim + 2 * lane) = pk;
 }
 
+// The same merge for many splits (long contexts): one 1024-thread workgroup
+// per (b, h) row.  Every thread reads lse values for the maximum; wave w then
+// accumulates splits w, w + 16, ... (eight partial rows in flight per lane)
+// and the sixteen waves' sums are merged through LDS.
+constexpr int kWideWaves = 16;
+constexpr int kWideThreshold = 16;  // splits above this use the wide merge
+
+template <typename T>
+__global__ __launch_bounds__(64 * kWideWaves) void decode_combine_wide_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_lse,
+    const int32_t* __restrict__ seqlens, uint16_t* __restrict__ out, int hq, int splits,
+    int split_tokens, int max_tokens) {
+  __shared__ float s_max[kWideWaves];
+  __shared__ float s_den[kWideWaves];
+  __shared__ __attribute__((aligned(16))) float s_o[kWideWaves][kHeadDim];
+  const int row = blockIdx.x;  // b * hq + h
+  const int b = row / hq;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int L = min(seqlens[b], max_tokens);
+  const int nvalid = L <= 0 ? 0 : min(splits, (L + split_tokens - 1) / split_tokens);
+  if (nvalid == 1) return;  // written by the split kernel
+  const float* lse = part_lse + (int64_t)row * splits;
+  float mx = -INFINITY;
+  for (int sp = tid; sp < nvalid; sp += 64 * kWideWaves) mx = fmaxf(mx, lse[sp]);
+#pragma unroll
+  for (int mask = 1; mask < 16; mask <<= 1) mx = wave_max_xor(mx, mask);
+  mx = max_xor32(max_xor16(mx));
+  if (lane == 0) s_max[wave] = mx;
+  __syncthreads();
+  float M = s_max[0];
+#pragma unroll
+  for (int w = 1; w < kWideWaves; ++w) M = fmaxf(M, s_max[w]);
+  float o0 = 0.0f, o1 = 0.0f, den = 0.0f;
+  if (M != -INFINITY) {
+    const float* po = part_o + (int64_t)row * splits * kHeadDim + 2 * lane;
+#pragma unroll 8
+    for (int sp = wave; sp < nvalid; sp += kWideWaves) {
+      const float w = exp2_fast(lse[sp] - M);
+      const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)sp * kHeadDim);
+      o0 += w * v.x;
+      o1 += w * v.y;
+      den += w;
+    }
+  }
+  s_o[wave][2 * lane] = o0;
+  s_o[wave][2 * lane + 1] = o1;
+  if (lane == 0) s_den[wave] = den;
+  __syncthreads();
+  if (wave != 0) return;
+  float a0 = 0.0f, a1 = 0.0f, d = 0.0f;
+#pragma unroll
+  for (int w = 0; w < kWideWaves; ++w) {
+    a0 += s_o[w][2 * lane];
+    a1 += s_o[w][2 * lane + 1];
+    d += s_den[w];
+  }
+  const float inv = d > 0.0f ? 1.0f / d : 0.0f;
+  const uint32_t pk = (uint32_t)Act<T>::from_f32(a0 * inv) |
+                      ((uint32_t)Act<T>::from_f32(a1 * inv) << 16);
+  *reinterpret_cast<uint32_t*>(out + (int64_t)row * kHeadDim + 2 * lane) = pk;
+}
+
 static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
 
 template <typename T>
@@ -370,9 +434,14 @@ static hipError_t launch_decode(const DecodeArgs& a, int batch,
   hipLaunchKernelGGL(decode_fp8_kernel<T>, grid, dim3(64 * kWavesPerWG), 0, stream, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
-  hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)(batch * a.hq)), dim3(64), 0,
-                     stream, a.part_o, a.part_lse, a.seqlens, a.out, a.hq, a.splits,
-                     a.pages_per_split * a.bs, a.w * a.bs);
+  if (a.splits > kWideThreshold)
+    hipLaunchKernelGGL(decode_combine_wide_kernel<T>, dim3((unsigned)(batch * a.hq)),
+                       dim3(64 * kWideWaves), 0, stream, a.part_o, a.part_lse, a.seqlens, a.out,
+                       a.hq, a.splits, a.pages_per_split * a.bs, a.w * a.bs);
+  else
+    hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)(batch * a.hq)), dim3(64), 0,
+                       stream, a.part_o, a.part_lse, a.seqlens, a.out, a.hq, a.splits,
+                       a.pages_per_split * a.bs, a.w * a.bs);
   return hipGetLastError();
 }
 
