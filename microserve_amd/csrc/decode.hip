@@ -341,10 +341,12 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(
   if (nvalid == 1) return;
   const float* lse = part_lse + (int64_t)row * splits;
   float M = -INFINITY;
+#pragma unroll 8
   for (int s = 0; s < nvalid; ++s) M = fmaxf(M, lse[s]);
   float o0 = 0.0f, o1 = 0.0f, den = 0.0f;
   if (M != -INFINITY) {
     const float* po = part_o + (int64_t)row * splits * kHeadDim + 2 * lane;
+#pragma unroll 8
     for (int s = 0; s < nvalid; ++s) {
       const float w = exp2_fast(lse[s] - M);
       const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kHeadDim);
@@ -364,7 +366,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(
 // accumulates splits w, w + 16, ... (eight partial rows in flight per lane)
 // and the sixteen waves' sums are merged through LDS.
 constexpr int kWideWaves = 16;
-constexpr int kWideThreshold = 16;  // splits above this use the wide merge
+constexpr int kWideThreshold = 64;  // splits above this use the wide merge
 
 template <typename T>
 __global__ __launch_bounds__(64 * kWideWaves) void decode_combine_wide_kernel(
