@@ -27,8 +27,9 @@
 //    group, lane i's element j comes from the address of lane 4j + i/4 plus
 //    2 * (i % 4) bytes.
 //  * P is rounded to the activation type for the PV MFMA (as flash-attn
-//    does) and l sums the rounded values, so each output is an exact convex
-//    combination of V rows under the weights applied.
+//    does) and l sums the rounded values (v_dot2 of each rounded pair with
+//    (1, 1)), so each output is an exact convex combination of V rows under
+//    the weights applied.
 //  * Online softmax in base 2 with a lazy rescale (slack 2^8; p <= 256 fits
 //    both fp16 and bf16); masks only on tiles that straddle the diagonal or
 //    the end of the keys; query blocks launch last-first.
@@ -46,6 +47,24 @@ constexpr int kDThreads = 64 * kDWaves;
 constexpr int kDRow = 2 * kHeadDim;  // bytes per K/V row
 constexpr int kDTile = kDStep * kDRow;
 constexpr float kDSlack = 8.0f;
+
+// Two probabilities rounded to the activation type, and l += their rounded
+// sum in fp32 with one v_dot2_f32_{bf16,f16} against (1, 1).
+template <typename T> struct PPair;
+template <> struct PPair<__bf16> {
+  typedef __bf16 t2 __attribute__((ext_vector_type(2)));
+  __device__ static t2 pack(float a, float b) { return t2{(__bf16)a, (__bf16)b}; }
+  __device__ static float acc(t2 v, float l) {
+    return __builtin_amdgcn_fdot2_f32_bf16(v, t2{(__bf16)1.0f, (__bf16)1.0f}, l, false);
+  }
+};
+template <> struct PPair<_Float16> {
+  typedef _Float16 t2 __attribute__((ext_vector_type(2)));
+  __device__ static t2 pack(float a, float b) { return t2{(_Float16)a, (_Float16)b}; }
+  __device__ static float acc(t2 v, float l) {
+    return __builtin_amdgcn_fdot2(v, t2{(_Float16)1.0f, (_Float16)1.0f}, l, false);
+  }
+};
 
 struct DenseArgs {
   const uint16_t* q;
@@ -227,10 +246,12 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const T p = (T)exp2_fast(fmaf(st[b][tt][r], a.scale_log2, -m_use));
-          psum += (float)p;
-          pv[b][tt >> 1][4 * (tt & 1) + r] = p;
+        for (int r = 0; r < 4; r += 2) {
+          const auto pk = PPair<T>::pack(exp2_fast(fmaf(st[b][tt][r], a.scale_log2, -m_use)),
+                                         exp2_fast(fmaf(st[b][tt][r + 1], a.scale_log2, -m_use)));
+          psum = PPair<T>::acc(pk, psum);
+          pv[b][tt >> 1][4 * (tt & 1) + r] = pk[0];
+          pv[b][tt >> 1][4 * (tt & 1) + r + 1] = pk[1];
         }
       l[b] += psum;
     }
