@@ -340,6 +340,128 @@ def time_fresh_prefill(dev, iters=10, warmup=2):
             "peak_tflops": BF16_PEAK_TFLOPS, "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
 
 
+class _Seq:
+    """The attributes of the runner's Sequence that its builders read."""
+
+    def __init__(self, token_ids, computed, scheduled, table, total=None):
+        self.token_ids = token_ids
+        self.num_computed_tokens = computed
+        self.num_scheduled_tokens = scheduled
+        self.block_table = table
+        self.gap = (len(token_ids) if total is None else total) - computed
+
+
+def _ragged_decode_seqs(seed=42, batch=256, pool=40000):
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    lens = np.exp(rng.uniform(np.log(16), np.log(32768), batch)).astype(np.int64)
+    perm = rng.permutation(pool)
+    seqs, at = [], 0
+    for n in lens.tolist():
+        pages = -(-n // BS)
+        seqs.append(_Seq(rng.integers(0, 151936, n).tolist(), n - 1, 1,
+                         perm[at:at + pages].tolist()))
+        at += pages
+    return seqs
+
+
+def _elementwise_decode_inputs(seqs, dev):
+    """The per-element device writes the runner's decode builder and block
+    table builder make (model_runner.py:124-142, 208-216): one host-to-device
+    copy per element and one per table row; timed as the path the device
+    builder replaces."""
+    n = len(seqs)
+    ids = torch.empty(n, dtype=torch.int64, device=dev)
+    pos = torch.empty(n, dtype=torch.int64, device=dev)
+    slot = torch.empty(n, dtype=torch.int64, device=dev)
+    lens = torch.empty(n, dtype=torch.int32, device=dev)
+    for i, s in enumerate(seqs):
+        p = s.num_computed_tokens
+        ids[i] = s.token_ids[p]
+        pos[i] = p
+        slot[i] = s.block_table[p // BS] * BS + p % BS
+        lens[i] = p + 1
+    width = max(len(s.block_table) for s in seqs)
+    tables = torch.full((n, width), -1, dtype=torch.int32, device=dev)
+    for i, s in enumerate(seqs):
+        if s.block_table:
+            tables[i, :len(s.block_table)] = torch.tensor(s.block_table, dtype=torch.int32,
+                                                          device=dev)
+    return ids, pos, slot, lens, tables
+
+
+def _elementwise_prefill_inputs(seqs, dev):
+    """The per-element device writes of the runner's prefill builder
+    (model_runner.py:144-172)."""
+    total = sum(s.num_scheduled_tokens for s in seqs)
+    ids = torch.empty(total, dtype=torch.int64, device=dev)
+    pos = torch.empty(total, dtype=torch.int64, device=dev)
+    slot = torch.empty(total, dtype=torch.int64, device=dev)
+    off = 0
+    for s in seqs:
+        for j in range(s.num_scheduled_tokens):
+            ids[off + j] = s.token_ids[j]
+            pos[off + j] = j
+            slot[off + j] = s.block_table[j // BS] * BS + j % BS
+        off += s.num_scheduled_tokens
+    return ids, pos, slot
+
+
+def _wall_us(fn, iters):
+    import statistics
+    times = []
+    for _ in range(iters):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        times.append((time.perf_counter() - t0) * 1e6)
+    return statistics.median(times)
+
+
+def time_step_inputs(dev, iters=30):
+    """Per-step input building: the device builder (one pinned copy + one
+    step_inputs_kernel launch) against the runner's element-by-element device
+    writes, each timed host wall clock to completion (median)."""
+    import numpy as np
+    from microserve_amd import step_inputs as SI
+    seqs = _ragged_decode_seqs()
+    SI.compile_decode(seqs, BS, dev)
+    dec_us = _wall_us(lambda: SI.compile_decode(seqs, BS, dev), iters)
+    width = max(len(s.block_table) for s in seqs)
+    gv = {"input_ids": torch.zeros(256, dtype=torch.int64, device=dev),
+          "positions": torch.zeros(256, dtype=torch.int64, device=dev),
+          "slot_mapping": torch.zeros(256, dtype=torch.int64, device=dev),
+          "cache_seqlens": torch.zeros(256, dtype=torch.int32, device=dev),
+          "block_tables": torch.zeros(256, width, dtype=torch.int32, device=dev)}
+    graph_us = _wall_us(lambda: SI.compile_decode(seqs[:200], BS, dev, pad_to=256,
+                                                  table_width=width, garbage_slot=40000 * BS,
+                                                  out=gv), iters)
+    _elementwise_decode_inputs(seqs, dev)
+    ref_dec_us = _wall_us(lambda: _elementwise_decode_inputs(seqs, dev), 3)
+    rng = np.random.default_rng(43)
+    pre = [_Seq(rng.integers(0, 151936, FRESH_LEN).tolist(), 0, FRESH_LEN,
+                list(range(i * (FRESH_LEN // BS), (i + 1) * (FRESH_LEN // BS))))
+           for i in range(FRESH_SEQS)]
+    SI.compile_prefill(pre, BS, dev)
+    pre_us = _wall_us(lambda: SI.compile_prefill(pre, BS, dev), 10)
+    sample = [_Seq(s.token_ids[:256], 0, 256, s.block_table[:1]) for s in pre]
+    _elementwise_prefill_inputs(sample, dev)
+    ref_sample_us = _wall_us(lambda: _elementwise_prefill_inputs(sample, dev), 3)
+    ref_pre_us = ref_sample_us * FRESH_LEN / 256
+    return {"decode": {"workload": "decode step, batch 256, context log-uniform on "
+                                   "[16, 32768], block 256, 40k-block pool",
+                       "us": round(dec_us, 1), "graph_padded_us": round(graph_us, 1),
+                       "elementwise_us": round(ref_dec_us, 1),
+                       "speedup": round(ref_dec_us / dec_us, 1)},
+            "prefill": {"workload": "fresh prefill step, 8 prompts x 8192 tokens, block 256",
+                        "us": round(pre_us, 1),
+                        "elementwise_us": round(ref_pre_us, 1),
+                        "elementwise_sample": "8 prompts x 256 tokens timed, scaled x32 "
+                                              "(linear in tokens)",
+                        "speedup": round(ref_pre_us / pre_us, 1)}}
+
+
 def calibrate_copy(dev, nbytes=1 << 30, iters=5):
     """A plain device copy of known size, for scaling the FETCH_SIZE and
     WRITE_SIZE counters to bytes (run it under rocprofv3 --pmc)."""
@@ -383,6 +505,8 @@ def main():
                     help="time only the fresh (unquantized) prefill workload")
     ap.add_argument("--shapes-only", action="store_true",
                     help="time only the ragged and long-context decode workloads")
+    ap.add_argument("--step-inputs-only", action="store_true",
+                    help="time only the per-step input builder")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run the 1 GiB copy used to calibrate rocprofv3 byte counters")
     args = ap.parse_args()
@@ -400,6 +524,9 @@ def main():
         return
     if args.fresh_only:
         print(json.dumps({"fresh_prefill": time_fresh_prefill(dev)}))
+        return
+    if args.step_inputs_only:
+        print(json.dumps({"step_inputs": time_step_inputs(dev)}))
         return
     if args.prefill_only:
         dtype = torch.bfloat16 if args.prefill_dtype == "bf16" else torch.float16
@@ -480,6 +607,7 @@ def main():
         torch.cuda.empty_cache()
         result["ragged"] = time_ragged(dev)
         result["long_context"] = [time_long_context(dev, b) for b in (1, 4)]
+        result["step_inputs"] = time_step_inputs(dev)
     print(json.dumps(result), flush=True)
 
 

@@ -167,6 +167,43 @@ int mskv_prefill_attention(const void* query, const void* key,
                            int num_q_heads, int num_kv_heads, int head_dim,
                            float softmax_scale, int act_dtype, void* stream);
 
+/*
+ * Expand one step's per-sequence scheduling state into its per-token inputs
+ * and -1-padded block tables, in one launch.
+ *
+ * Replaces the element-by-element device writes of ModelRunner's
+ * _compile_decode / _compile_prefill / _compile_chunk_prefill /
+ * _make_block_tables (microserve/engine/model_runner.py:124-193, 208-216)
+ * and the graph padding of _run_decode (:264-272).  Sequence b schedules
+ * n_b = cu_seqlens_q[b+1] - cu_seqlens_q[b] positions p = seq_start[b] + j;
+ * row r = cu_seqlens_q[b] + j gets input_ids[r] = token_ids[r],
+ * positions[r] = p and slot_mapping[r] = table_b[p / block_size] *
+ * block_size + p % block_size, or -1 when p / block_size is past the end of
+ * table_b (the reference raises there; the store skips -1).  table_b is
+ * tables[table_offsets[b] .. table_offsets[b+1]).  cache_seqlens[b] =
+ * seq_start[b] + n_b; block_tables[b][c] = table_b[c] for c < len_b, else
+ * -1, for c < table_width.  Rows b = num_seqs .. pad_seqs - 1 are padding
+ * rows of a captured decode graph: slot_mapping / input_ids / positions row
+ * total_q + (b - num_seqs) get garbage_slot / 0 / 0, cache_seqlens[b] = 0
+ * and the table row is -1.
+ * token_ids: int64 [total_q]; seq_start: int32 [num_seqs]; cu_seqlens_q and
+ * table_offsets: nondecreasing int32 [num_seqs + 1] starting at 0, with
+ * cu_seqlens_q[num_seqs] == total_q; tables: int32 [table_offsets[num_seqs]].
+ * Outputs input_ids, positions, slot_mapping: int64 [total_q + pad_seqs -
+ * num_seqs] (NULL allowed when that is 0); cache_seqlens: int32 [pad_seqs]
+ * or NULL; block_tables: int32 [pad_seqs, table_width] or NULL.
+ * max_seqlen_q only sizes the launch.
+ */
+int mskv_build_step_inputs(const int64_t* token_ids, const int32_t* seq_start,
+                           const int32_t* cu_seqlens_q,
+                           const int32_t* table_offsets, const int32_t* tables,
+                           int num_seqs, int pad_seqs, int64_t total_q,
+                           int block_size, int table_width,
+                           int64_t garbage_slot, int64_t* input_ids,
+                           int64_t* positions, int64_t* slot_mapping,
+                           int32_t* cache_seqlens, int32_t* block_tables,
+                           int max_seqlen_q, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

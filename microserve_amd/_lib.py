@@ -42,6 +42,9 @@ _PROTOS = {
     "mskv_prefill_attention": (_c_int, [
         _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_i64, _c_int,
         _c_int, _c_int, _c_int, _c_f32, _c_int, _vp]),
+    "mskv_build_step_inputs": (_c_int, [
+        _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_i64, _c_int, _c_int, _c_i64,
+        _vp, _vp, _vp, _vp, _vp, _c_int, _vp]),
 }
 
 EXPORTED = tuple(_PROTOS)
