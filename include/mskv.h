@@ -204,6 +204,49 @@ int mskv_build_step_inputs(const int64_t* token_ids, const int32_t* seq_start,
                            int32_t* cache_seqlens, int32_t* block_tables,
                            int max_seqlen_q, void* stream);
 
+/*
+ * Fused attention prologue: per-head RMSNorm of q and k, rotary embedding,
+ * and the FP8 store of the rotated k and of v, in one launch.
+ *
+ * Replaces microserve/models/qwen3.py:49-53 (q_norm, k_norm, rotary_emb)
+ * and the store_fp8_kvcache call that opens Attention.forward
+ * (microserve/layers/attention.py:41-43).  For each token t and head row x
+ * of q (num_q_heads rows) and k (num_kv_heads rows), in act_dtype T:
+ *   RMSNorm (microserve/layers/layernorm.py:55-57, 80-81), skipped when both
+ *   weights are NULL: var = (sum of x^2) / 128 in fp32, summed as eight
+ *   partial sums (lane l: elements 8l..8l+7 then 64+8l..64+8l+7, in order)
+ *   combined as ((s0+s1)+(s2+s3))+((s4+s5)+(s6+s7)); r = 1/sqrtf(var + eps)
+ *   with IEEE fp32 sqrt and division; y = T(T(x * r) * w).
+ *   Rotary (microserve/layers/rotary_embedding.py:24-31), p = positions[t],
+ *   c = cos_cache[p], s = sin_cache[p], for d < 64:
+ *   out[d] = T(T(y[d]*c[d]) + T(-y[d+64]*s[d])),
+ *   out[d+64] = T(T(y[d+64]*c[d+64]) + T(y[d]*s[d+64])), sums in fp32 first.
+ * q rows go to q_out; k rows to k_out (if not NULL) and, with the v rows, to
+ * the FP8 cache at slot_mapping[t] with the bytes and scales of
+ * mskv_store_fp8_kvcache.  A token with p outside [0, max_position) gets zero
+ * q_out/k_out rows and is not stored; slots outside [0, num_slots) are
+ * skipped.
+ * q/k/v: [num_tokens, heads, 128] in act_dtype with heads contiguous and
+ * the given token strides (elements; views of one qkv tensor allowed);
+ * positions: int64 [num_tokens]; weights: act_dtype [128];
+ * cos_cache/sin_cache: act_dtype [max_position, 128]; q_out: [num_tokens,
+ * num_q_heads, 128]; k_out: [num_tokens, num_kv_heads, 128] or NULL.  Every
+ * tensor must be 16-byte aligned and token strides multiples of 8.
+ * Supported: head_dim == 128.
+ */
+int mskv_qk_norm_rope_store(const void* q, const void* k, const void* v,
+                            int64_t q_token_stride, int64_t k_token_stride,
+                            int64_t v_token_stride, const int64_t* positions,
+                            const void* q_norm_weight, const void* k_norm_weight,
+                            float eps, const void* cos_cache,
+                            const void* sin_cache, int64_t max_position,
+                            void* q_out, void* k_out, void* k_cache,
+                            void* v_cache, float* k_scale_cache,
+                            float* v_scale_cache, const void* slot_mapping,
+                            int slot_dtype, int64_t num_tokens, int num_q_heads,
+                            int num_kv_heads, int head_dim, int64_t num_slots,
+                            int act_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -45,6 +45,10 @@ _PROTOS = {
     "mskv_build_step_inputs": (_c_int, [
         _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_i64, _c_int, _c_int, _c_i64,
         _vp, _vp, _vp, _vp, _vp, _c_int, _vp]),
+    "mskv_qk_norm_rope_store": (_c_int, [
+        _vp, _vp, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _c_f32, _vp, _vp, _c_i64,
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_i64,
+        _c_int, _vp]),
 }
 
 EXPORTED = tuple(_PROTOS)

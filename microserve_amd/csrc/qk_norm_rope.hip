@@ -1,0 +1,252 @@
+// Fused attention prologue: per-head RMSNorm of q and k, rotary embedding,
+// and the FP8 store of k and v, in one pass over the qkv projection output.
+//
+// Replaces microserve/models/qwen3.py:49-53 followed by the store at the top
+// of Attention.forward (microserve/layers/attention.py:41-43):
+//   q = q_norm(q); k = k_norm(k); q, k = rotary_emb(positions, q, k)
+//   store_fp8_kvcache(k, v, ...)
+// The unfused chain reads and writes q and k several times in fp32 and
+// 16-bit temporaries; here each q/k/v row is read once, q (and, for the fresh
+// prefill that attends over the unquantized keys, k) is written once, and k
+// and v go to the cache as FP8 in the same pass.
+//
+// Arithmetic, every step rounded as the reference's torch ops round it (the
+// runner casts the model, norm weights and rotary tables included, to the
+// activation type: microserve/engine/model_runner.py:58-59):
+//   RMSNorm (microserve/layers/layernorm.py:55-57, 80-81):
+//     var = sum(x^2) / 128 in fp32; r = 1 / sqrt(var + eps), both IEEE fp32;
+//     n = T(x * r); y = T(n * w).
+//   The sum order is fixed: lane l of the row's 8 lanes sums its 16 squares
+//   in order, then ((s0+s1)+(s2+s3)) + ((s4+s5)+(s6+s7)).  (torch does not
+//   specify its reduction order or its rsqrt rounding; this order and the
+//   correctly rounded 1/sqrt are the definition the results are exact to.)
+//   Rotary (microserve/layers/rotary_embedding.py:4-7, 24-31), for d < 64:
+//     out[d]      = T(T(y[d] * cos[d])           + T(-y[d+64] * sin[d]))
+//     out[d + 64] = T(T(y[d+64] * cos[d+64])     + T(y[d] * sin[d+64]))
+//   with each sum taken in fp32 first, as torch's 16-bit add does.
+//   Store: the bytes and scales of store_fp8_kvcache on the rotated k and on
+//   v (microserve/layers/fp8_kv_cache.py:11-39).
+//
+// Work layout: eight lanes own one (token, row) pair, row = one of the
+// num_q_heads + 2 * num_kv_heads heads of the token; lane l holds elements
+// [8l, 8l+8) and [64+8l, 64+8l+8), so rotate_half's pairs (d, d+64) meet in
+// one lane and the only cross-lane traffic is the two DPP reductions.
+#include <math.h>
+
+#include "fp8_row.h"
+#include "mskv_device.h"
+#include "../../include/mskv.h"
+
+namespace mskv {
+
+constexpr int kNrThreads = 256;
+constexpr int kNrRowsPerBlock = kNrThreads / 8;
+
+struct NormRopeArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  int64_t q_stride, k_stride, v_stride;  // elements between tokens
+  const int64_t* positions;
+  const uint16_t* q_weight;  // NULL: no norm (rotary only)
+  const uint16_t* k_weight;
+  const uint16_t* cos;  // [max_position, 128]
+  const uint16_t* sin;
+  uint16_t* q_out;  // [tokens, hq, 128]
+  uint16_t* k_out;  // [tokens, hk, 128] or NULL
+  uint8_t* k_cache;
+  uint8_t* v_cache;
+  float* k_scale;
+  float* v_scale;
+  const void* slots;
+  int64_t rows, num_slots, max_position;
+  int hq, hk, heads;
+  float eps;
+};
+
+// Sum over the 8 lanes of a row group: xor 1, xor 2, then the mirrored
+// lane of the other quad.  Addition is commutative, so every lane ends with
+// the same bits: ((s0+s1)+(s2+s3)) + ((s4+s5)+(s6+s7)).
+__device__ __forceinline__ float sum8_dpp(float v) {
+  int x = __float_as_int(v);
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false));
+  x = __float_as_int(v);
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false));
+  x = __float_as_int(v);
+  v = v + __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false));
+  return v;
+}
+
+template <typename T>
+__device__ __forceinline__ float rnd(float x) {
+  return (float)(T)x;
+}
+
+// T(x) of a value that must first be rounded to fp32, as torch rounds x * r
+// before casting.  For fp16 the backend would otherwise fold the multiply
+// and the cast into one v_fma_mixlo_f16, which rounds once, and that differs
+// where the fp32 product lies on an fp16 tie.  (Products of two 16-bit
+// values are exact in fp32 and sums of two fp16 values round innocuously
+// twice, so only this product needs it.)
+template <typename T>
+__device__ __forceinline__ float rnd_f32(float x) {
+  asm volatile("" : "+v"(x));
+  return (float)(T)x;
+}
+
+template <typename T>
+__device__ __forceinline__ void unpack8(const u32x4& a, float* x) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    x[2 * i] = Act<T>::to_f32((uint16_t)(a[i] & 0xFFFFu));
+    x[2 * i + 1] = Act<T>::to_f32((uint16_t)(a[i] >> 16));
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ u32x4 pack8(const float* x) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    r[i] = (uint32_t)Act<T>::from_f32(x[2 * i]) | ((uint32_t)Act<T>::from_f32(x[2 * i + 1]) << 16);
+  return r;
+}
+
+template <typename T, typename SlotT>
+__global__ __launch_bounds__(kNrThreads) void qk_norm_rope_store_kernel(NormRopeArgs a) {
+#pragma clang fp contract(off)
+  const int sub = threadIdx.x & 7;
+  const int64_t row = (int64_t)blockIdx.x * kNrRowsPerBlock + (threadIdx.x >> 3);
+  if (row >= a.rows) return;  // whole 8-lane groups leave together
+  const int64_t tok = row / a.heads;
+  const int j = (int)(row - tok * a.heads);
+  const int64_t pos = a.positions[tok];
+  const bool pos_ok = pos >= 0 && pos < a.max_position;
+  const int lo = 8 * sub, hi = kHeadDim / 2 + 8 * sub;
+
+  const uint16_t* src;
+  if (j < a.hq)
+    src = a.q + tok * a.q_stride + (int64_t)j * kHeadDim;
+  else if (j < a.hq + a.hk)
+    src = a.k + tok * a.k_stride + (int64_t)(j - a.hq) * kHeadDim;
+  else
+    src = a.v + tok * a.v_stride + (int64_t)(j - a.hq - a.hk) * kHeadDim;
+  float x[16];
+  unpack8<T>(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + lo)), x);
+  unpack8<T>(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + hi)), x + 8);
+
+  const bool is_v = j >= a.hq + a.hk;
+  if (!is_v) {
+    const uint16_t* w = j < a.hq ? a.q_weight : a.k_weight;
+    if (w) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) ss += x[i] * x[i];  // each square is exact
+      const float var = sum8_dpp(ss) / (float)kHeadDim;
+      const float r = 1.0f / sqrtf(var + a.eps);
+      float wv[16];
+      unpack8<T>(*reinterpret_cast<const u32x4*>(w + lo), wv);
+      unpack8<T>(*reinterpret_cast<const u32x4*>(w + hi), wv + 8);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = rnd<T>(rnd_f32<T>(x[i] * r) * wv[i]);
+    }
+    float c[16], s[16];
+    const int64_t tab = (pos_ok ? pos : 0) * kHeadDim;
+    unpack8<T>(*reinterpret_cast<const u32x4*>(a.cos + tab + lo), c);
+    unpack8<T>(*reinterpret_cast<const u32x4*>(a.cos + tab + hi), c + 8);
+    unpack8<T>(*reinterpret_cast<const u32x4*>(a.sin + tab + lo), s);
+    unpack8<T>(*reinterpret_cast<const u32x4*>(a.sin + tab + hi), s + 8);
+    float o[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      o[i] = rnd<T>(rnd<T>(x[i] * c[i]) + (-rnd<T>(x[8 + i] * s[i])));
+      o[8 + i] = rnd<T>(rnd<T>(x[8 + i] * c[8 + i]) + rnd<T>(x[i] * s[8 + i]));
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = pos_ok ? o[i] : 0.0f;
+    uint16_t* dst = nullptr;
+    if (j < a.hq)
+      dst = a.q_out + (tok * a.hq + j) * kHeadDim;
+    else if (a.k_out)
+      dst = a.k_out + (tok * a.hk + (j - a.hq)) * kHeadDim;
+    if (dst) {
+      *reinterpret_cast<u32x4*>(dst + lo) = pack8<T>(x);
+      *reinterpret_cast<u32x4*>(dst + hi) = pack8<T>(x + 8);
+    }
+    if (j < a.hq) return;
+  }
+
+  // k (rotated) or v: FP8 row and its scale
+  u32x4 qb;
+  const float scale = quantize16(x, qb);
+  const int64_t slot = (int64_t)static_cast<const SlotT*>(a.slots)[tok];
+  if (!pos_ok || slot < 0 || slot >= a.num_slots) return;
+  const int head = is_v ? j - a.hq - a.hk : j - a.hq;
+  const int64_t dst = slot * a.hk + head;
+  uint8_t* cache = is_v ? a.v_cache : a.k_cache;
+  *reinterpret_cast<u32x2*>(cache + dst * kHeadDim + lo) = u32x2{qb[0], qb[1]};
+  *reinterpret_cast<u32x2*>(cache + dst * kHeadDim + hi) = u32x2{qb[2], qb[3]};
+  if (sub == 0) (is_v ? a.v_scale : a.k_scale)[dst] = scale;
+}
+
+template <typename T>
+static hipError_t launch_norm_rope(const NormRopeArgs& a, int slot_dtype, hipStream_t stream) {
+  const int64_t blocks = (a.rows + kNrRowsPerBlock - 1) / kNrRowsPerBlock;
+  if (slot_dtype == MSKV_INT64)
+    hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, int64_t>), dim3((unsigned)blocks),
+                       dim3(kNrThreads), 0, stream, a);
+  else
+    hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, int32_t>), dim3((unsigned)blocks),
+                       dim3(kNrThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+}  // namespace mskv
+
+extern "C" int mskv_qk_norm_rope_store(
+    const void* q, const void* k, const void* v, int64_t q_token_stride,
+    int64_t k_token_stride, int64_t v_token_stride, const int64_t* positions,
+    const void* q_norm_weight, const void* k_norm_weight, float eps, const void* cos_cache,
+    const void* sin_cache, int64_t max_position, void* q_out, void* k_out, void* k_cache,
+    void* v_cache, float* k_scale_cache, float* v_scale_cache, const void* slot_mapping,
+    int slot_dtype, int64_t num_tokens, int num_q_heads, int num_kv_heads, int head_dim,
+    int64_t num_slots, int act_dtype, void* stream) {
+  if (num_tokens < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || num_slots < 0 ||
+      max_position <= 0)
+    return MSKV_EINVAL;
+  if (slot_dtype != MSKV_INT32 && slot_dtype != MSKV_INT64) return MSKV_EINVAL;
+  if (act_dtype != MSKV_FLOAT16 && act_dtype != MSKV_BFLOAT16) return MSKV_EINVAL;
+  if (head_dim != mskv::kHeadDim) return MSKV_EUNSUPPORTED;
+  if ((q_norm_weight == nullptr) != (k_norm_weight == nullptr)) return MSKV_EINVAL;
+  if (!(eps >= 0.0f)) return MSKV_EINVAL;
+  if (num_tokens == 0) return MSKV_OK;
+  if (!q || !k || !v || !positions || !cos_cache || !sin_cache || !q_out || !k_cache ||
+      !v_cache || !k_scale_cache || !v_scale_cache || !slot_mapping)
+    return MSKV_EINVAL;
+  if (q_token_stride < (int64_t)num_q_heads * head_dim ||
+      k_token_stride < (int64_t)num_kv_heads * head_dim ||
+      v_token_stride < (int64_t)num_kv_heads * head_dim)
+    return MSKV_EINVAL;
+  // 16-byte loads and stores: every row must start 16-byte aligned
+  auto misaligned = [](const void* p) { return ((uintptr_t)p & 15u) != 0; };
+  if (misaligned(q) || misaligned(k) || misaligned(v) || misaligned(q_out) ||
+      (k_out && misaligned(k_out)) || misaligned(cos_cache) || misaligned(sin_cache) ||
+      (q_norm_weight && (misaligned(q_norm_weight) || misaligned(k_norm_weight))) ||
+      (q_token_stride | k_token_stride | v_token_stride) % 8 != 0)
+    return MSKV_EINVAL;
+  const int heads = num_q_heads + 2 * num_kv_heads;
+  const int64_t rows = num_tokens * heads;
+  if ((rows + mskv::kNrRowsPerBlock - 1) / mskv::kNrRowsPerBlock > 0x7FFFFFFFLL)
+    return MSKV_EUNSUPPORTED;
+  mskv::NormRopeArgs a{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
+                       q_token_stride, k_token_stride, v_token_stride, positions,
+                       (const uint16_t*)q_norm_weight, (const uint16_t*)k_norm_weight,
+                       (const uint16_t*)cos_cache, (const uint16_t*)sin_cache,
+                       (uint16_t*)q_out, (uint16_t*)k_out, (uint8_t*)k_cache,
+                       (uint8_t*)v_cache, k_scale_cache, v_scale_cache, slot_mapping, rows,
+                       num_slots, max_position, num_q_heads, num_kv_heads, heads, eps};
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const hipError_t e = act_dtype == MSKV_BFLOAT16 ? mskv::launch_norm_rope<__bf16>(a, slot_dtype, s)
+                                                   : mskv::launch_norm_rope<_Float16>(a, slot_dtype, s);
+  return (int)e;
+}
