@@ -462,6 +462,101 @@ def time_step_inputs(dev, iters=30):
                         "speedup": round(ref_pre_us / pre_us, 1)}}
 
 
+def norm_rope_bytes(n, hq, hk, with_k, act=2):
+    """Algorithmic HBM bytes of the fused prologue for n tokens: q/k/v rows
+    read once, cos/sin rows once per token, positions and slots; q (and k)
+    written once, k/v FP8 rows and their scales."""
+    rd = n * ((hq + 2 * hk) * D * act + 2 * D * act + 8 + 8)
+    wr = n * (hq * D * act + (hk * D * act if with_k else 0) + 2 * hk * D + 2 * hk * 4)
+    return rd + wr
+
+
+def _unfused_prologue(positions, q, k, v, qw, kw, eps, cos, sin, cache, slots):
+    """The reference's chain on the GPU (microserve/models/qwen3.py:49-53 with
+    layernorm.py:55-57,80-81 and rotary_embedding.py:24-31, then the store at
+    attention.py:41-43): torch ops for the norms and the rotation, this
+    library's store kernel for the cache."""
+    from microserve_amd import store_fp8_kvcache
+
+    def norm(x, w):
+        xf = x.float()
+        return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)).to(x.dtype) * w
+
+    def rot(x):
+        x1, x2 = x.chunk(2, dim=-1)
+        return torch.cat((-x2, x1), dim=-1)
+
+    q, k = norm(q, qw), norm(k, kw)
+    c = cos[positions].unsqueeze(1)
+    s_ = sin[positions].unsqueeze(1)
+    q, k = (q * c) + (rot(q) * s_), (k * c) + (rot(k) * s_)
+    store_fp8_kvcache(k, v, *cache, slots)
+    return q, k
+
+
+def time_norm_rope(dev, iters=20, warmup=3):
+    """Fused q/k RMSNorm + rotary + FP8 store against the reference's unfused
+    torch chain (plus the store kernel), Qwen3-8B heads, bf16."""
+    from microserve_amd import qk_norm_rope_store
+    gen = torch.Generator().manual_seed(77)
+    cos_t, sin_t = _rope_tables_bf16(40960)
+    cos_t, sin_t = cos_t.to(dev), sin_t.to(dev)
+    out = []
+    for n, mode in ((FRESH_SEQS * FRESH_LEN, "prefill"), (BATCH, "decode")):
+        qkv = torch.randn(n, (HQ + 2 * HK) * D, generator=gen).bfloat16().to(dev)
+        q, k, v = (t.view(n, -1, D) for t in qkv.split([HQ * D, HK * D, HK * D], dim=-1))
+        pos = torch.randint(0, 40960, (n,), generator=gen).to(dev)
+        qw = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16().to(dev)
+        kw = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16().to(dev)
+        nb = max(1, -(-n // BS))
+        slots = torch.randperm(nb * BS, generator=gen)[:n].to(dev)
+        cache = (torch.zeros(nb, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev),
+                 torch.zeros(nb, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev),
+                 torch.ones(nb, BS, HK, device=dev), torch.ones(nb, BS, HK, device=dev))
+        with_k = mode == "prefill"
+
+        def fused():
+            return qk_norm_rope_store(pos, q, k, v, qw, kw, 1e-6, cos_t, sin_t, *cache, slots,
+                                      return_k=with_k)
+
+        def unfused():
+            return _unfused_prologue(pos, q, k, v, qw, kw, 1e-6, cos_t, sin_t, cache, slots)
+
+        res = {}
+        for name, fn in (("fused", fused), ("unfused", unfused)):
+            # back-to-back calls between two events: the device time per call
+            # when the GPU outruns the host (the large step), the per-call
+            # host cost when it does not (the 64-token step)
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            stream = torch.cuda.current_stream()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            for _ in range(iters):
+                fn()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            res[name] = e0.elapsed_time(e1) / iters * 1e3
+        nbytes = norm_rope_bytes(n, HQ, HK, with_k)
+        out.append({"workload": f"{mode}: {n} tokens, 32 q / 8 kv heads, bf16, rotary table "
+                                f"40960 x 128",
+                    "us": round(res["fused"], 2), "unfused_us": round(res["unfused"], 2),
+                    "speedup": round(res["unfused"] / res["fused"], 2),
+                    "bytes": nbytes, "gbs": round(nbytes / res["fused"] / 1e3, 1),
+                    "frac": round(nbytes / res["fused"] / 1e3 / HBM_PEAK_GBS, 4)})
+    return out
+
+
+def _rope_tables_bf16(max_position, base=1e6):
+    """cos/sin tables as the reference builds them (rotary_embedding.py:16-22)
+    after the runner's cast to the activation type."""
+    inv_freq = 1.0 / (base ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    freqs = torch.einsum("i,j -> ij", torch.arange(max_position, dtype=torch.float32), inv_freq)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    return emb.cos().bfloat16(), emb.sin().bfloat16()
+
+
 def calibrate_copy(dev, nbytes=1 << 30, iters=5):
     """A plain device copy of known size, for scaling the FETCH_SIZE and
     WRITE_SIZE counters to bytes (run it under rocprofv3 --pmc)."""
@@ -505,6 +600,8 @@ def main():
                     help="time only the fresh (unquantized) prefill workload")
     ap.add_argument("--shapes-only", action="store_true",
                     help="time only the ragged and long-context decode workloads")
+    ap.add_argument("--norm-rope-only", action="store_true",
+                    help="time only the fused q/k norm + rotary + store prologue")
     ap.add_argument("--step-inputs-only", action="store_true",
                     help="time only the per-step input builder")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -524,6 +621,9 @@ def main():
         return
     if args.fresh_only:
         print(json.dumps({"fresh_prefill": time_fresh_prefill(dev)}))
+        return
+    if args.norm_rope_only:
+        print(json.dumps({"qk_norm_rope_store": time_norm_rope(dev)}))
         return
     if args.step_inputs_only:
         print(json.dumps({"step_inputs": time_step_inputs(dev)}))
@@ -608,6 +708,7 @@ def main():
         result["ragged"] = time_ragged(dev)
         result["long_context"] = [time_long_context(dev, b) for b in (1, 4)]
         result["step_inputs"] = time_step_inputs(dev)
+        result["qk_norm_rope_store"] = time_norm_rope(dev)
     print(json.dumps(result), flush=True)
 
 

@@ -40,7 +40,8 @@
 namespace mskv {
 
 constexpr int kNrThreads = 256;
-constexpr int kNrRowsPerBlock = kNrThreads / 8;
+constexpr int kNrRowsPerBlock = kNrThreads / 8;  // rows in flight per pass
+constexpr int kNrRowsPerGroup = 2;
 
 struct NormRopeArgs {
   const uint16_t* q;
@@ -112,29 +113,13 @@ __device__ __forceinline__ u32x4 pack8(const float* x) {
   return r;
 }
 
-template <typename T, typename SlotT>
-__global__ __launch_bounds__(kNrThreads) void qk_norm_rope_store_kernel(NormRopeArgs a) {
+// One row: x holds its 16 elements (lane layout above), already loaded.
+template <typename T>
+__device__ __forceinline__ void finish_row(const NormRopeArgs& a, int64_t tok, int j, int64_t pos,
+                                           int64_t slot, int sub, float* x) {
 #pragma clang fp contract(off)
-  const int sub = threadIdx.x & 7;
-  const int64_t row = (int64_t)blockIdx.x * kNrRowsPerBlock + (threadIdx.x >> 3);
-  if (row >= a.rows) return;  // whole 8-lane groups leave together
-  const int64_t tok = row / a.heads;
-  const int j = (int)(row - tok * a.heads);
-  const int64_t pos = a.positions[tok];
   const bool pos_ok = pos >= 0 && pos < a.max_position;
   const int lo = 8 * sub, hi = kHeadDim / 2 + 8 * sub;
-
-  const uint16_t* src;
-  if (j < a.hq)
-    src = a.q + tok * a.q_stride + (int64_t)j * kHeadDim;
-  else if (j < a.hq + a.hk)
-    src = a.k + tok * a.k_stride + (int64_t)(j - a.hq) * kHeadDim;
-  else
-    src = a.v + tok * a.v_stride + (int64_t)(j - a.hq - a.hk) * kHeadDim;
-  float x[16];
-  unpack8<T>(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + lo)), x);
-  unpack8<T>(__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + hi)), x + 8);
-
   const bool is_v = j >= a.hq + a.hk;
   if (!is_v) {
     const uint16_t* w = j < a.hq ? a.q_weight : a.k_weight;
@@ -170,8 +155,8 @@ __global__ __launch_bounds__(kNrThreads) void qk_norm_rope_store_kernel(NormRope
     else if (a.k_out)
       dst = a.k_out + (tok * a.hk + (j - a.hq)) * kHeadDim;
     if (dst) {
-      *reinterpret_cast<u32x4*>(dst + lo) = pack8<T>(x);
-      *reinterpret_cast<u32x4*>(dst + hi) = pack8<T>(x + 8);
+      __builtin_nontemporal_store(pack8<T>(x), reinterpret_cast<u32x4*>(dst + lo));
+      __builtin_nontemporal_store(pack8<T>(x + 8), reinterpret_cast<u32x4*>(dst + hi));
     }
     if (j < a.hq) return;
   }
@@ -179,19 +164,64 @@ __global__ __launch_bounds__(kNrThreads) void qk_norm_rope_store_kernel(NormRope
   // k (rotated) or v: FP8 row and its scale
   u32x4 qb;
   const float scale = quantize16(x, qb);
-  const int64_t slot = (int64_t)static_cast<const SlotT*>(a.slots)[tok];
   if (!pos_ok || slot < 0 || slot >= a.num_slots) return;
   const int head = is_v ? j - a.hq - a.hk : j - a.hq;
   const int64_t dst = slot * a.hk + head;
   uint8_t* cache = is_v ? a.v_cache : a.k_cache;
-  *reinterpret_cast<u32x2*>(cache + dst * kHeadDim + lo) = u32x2{qb[0], qb[1]};
-  *reinterpret_cast<u32x2*>(cache + dst * kHeadDim + hi) = u32x2{qb[2], qb[3]};
+  __builtin_nontemporal_store(u32x2{qb[0], qb[1]},
+                              reinterpret_cast<u32x2*>(cache + dst * kHeadDim + lo));
+  __builtin_nontemporal_store(u32x2{qb[2], qb[3]},
+                              reinterpret_cast<u32x2*>(cache + dst * kHeadDim + hi));
   if (sub == 0) (is_v ? a.v_scale : a.k_scale)[dst] = scale;
+}
+
+// Each 8-lane group owns kNrRowsPerGroup rows, kNrRowsPerBlock apart, and
+// issues the loads of all of them before finishing the first: twice the
+// bytes in flight per lane at the same occupancy.
+template <typename T, typename SlotT>
+__global__ __launch_bounds__(kNrThreads) void qk_norm_rope_store_kernel(NormRopeArgs a) {
+  const int sub = threadIdx.x & 7;
+  const int64_t first = (int64_t)blockIdx.x * (kNrRowsPerBlock * kNrRowsPerGroup) +
+                        (threadIdx.x >> 3);
+  const int lo = 8 * sub, hi = kHeadDim / 2 + 8 * sub;
+  int64_t tok[kNrRowsPerGroup], pos[kNrRowsPerGroup], slot[kNrRowsPerGroup];
+  int jj[kNrRowsPerGroup];
+  u32x4 xl[kNrRowsPerGroup], xh[kNrRowsPerGroup];
+#pragma unroll
+  for (int u = 0; u < kNrRowsPerGroup; ++u) {
+    const int64_t row = first + (int64_t)u * kNrRowsPerBlock;
+    if (row >= a.rows) break;  // whole 8-lane groups leave together
+    // rows < 2^31 (checked on the host): 32-bit division
+    const uint32_t t32 = (uint32_t)row / (uint32_t)a.heads;
+    tok[u] = t32;
+    const int j = (int)((uint32_t)row - t32 * (uint32_t)a.heads);
+    jj[u] = j;
+    const uint16_t* src;
+    if (j < a.hq)
+      src = a.q + tok[u] * a.q_stride + (int64_t)j * kHeadDim;
+    else if (j < a.hq + a.hk)
+      src = a.k + tok[u] * a.k_stride + (int64_t)(j - a.hq) * kHeadDim;
+    else
+      src = a.v + tok[u] * a.v_stride + (int64_t)(j - a.hq - a.hk) * kHeadDim;
+    xl[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + lo));
+    xh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + hi));
+    pos[u] = a.positions[tok[u]];
+    slot[u] = j < a.hq ? 0 : (int64_t)static_cast<const SlotT*>(a.slots)[tok[u]];
+  }
+#pragma unroll
+  for (int u = 0; u < kNrRowsPerGroup; ++u) {
+    if (first + (int64_t)u * kNrRowsPerBlock >= a.rows) return;
+    float x[16];
+    unpack8<T>(xl[u], x);
+    unpack8<T>(xh[u], x + 8);
+    finish_row<T>(a, tok[u], jj[u], pos[u], slot[u], sub, x);
+  }
 }
 
 template <typename T>
 static hipError_t launch_norm_rope(const NormRopeArgs& a, int slot_dtype, hipStream_t stream) {
-  const int64_t blocks = (a.rows + kNrRowsPerBlock - 1) / kNrRowsPerBlock;
+  const int64_t per_block = (int64_t)kNrRowsPerBlock * kNrRowsPerGroup;
+  const int64_t blocks = (a.rows + per_block - 1) / per_block;
   if (slot_dtype == MSKV_INT64)
     hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, int64_t>), dim3((unsigned)blocks),
                        dim3(kNrThreads), 0, stream, a);
@@ -236,8 +266,7 @@ extern "C" int mskv_qk_norm_rope_store(
     return MSKV_EINVAL;
   const int heads = num_q_heads + 2 * num_kv_heads;
   const int64_t rows = num_tokens * heads;
-  if ((rows + mskv::kNrRowsPerBlock - 1) / mskv::kNrRowsPerBlock > 0x7FFFFFFFLL)
-    return MSKV_EUNSUPPORTED;
+  if (rows > 0x7FFFFFFFLL) return MSKV_EUNSUPPORTED;
   mskv::NormRopeArgs a{(const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v,
                        q_token_stride, k_token_stride, v_token_stride, positions,
                        (const uint16_t*)q_norm_weight, (const uint16_t*)k_norm_weight,
