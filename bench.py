@@ -687,7 +687,7 @@ def main():
                    "launch": "eager, one decode call per step",
                    "algorithmic_bytes_per_step": nbytes},
         "pct_of_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "roofline": {"bound": "hbm", "kernel": "decode_fp8_kernel + decode_combine_kernel",
+        "roofline": {"bound": "hbm", "kernel": "decode_fp8_kernel + decode_combine_small_kernel",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "avg_launch_us": round(avg_launch * 1e6, 2),

@@ -361,6 +361,57 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(
   *reinterpret_cast<uint32_t*>(out + (int64_t)row * kHeadDim + 2 * lane) = pk;
 }
 
+// The same merge for at most S splits (S a compile-time bound, small): every
+// split's lse value and partial row is loaded at once, before the sequence
+// length arrives, so a row costs one memory round trip instead of three.
+// Rows of few splits use them all; with many splits, mostly unused (ragged
+// batches), the reads of unused rows cost more than the round trips, so
+// those keep decode_combine_kernel.  The arithmetic is
+// decode_combine_kernel's, operation for operation.
+template <typename T, int S>
+__global__ __launch_bounds__(64) void decode_combine_small_kernel(
+    const float* __restrict__ part_o, const float* __restrict__ part_lse,
+    const int32_t* __restrict__ seqlens, uint16_t* __restrict__ out, int hq,
+    int splits, int split_tokens, int max_tokens) {
+  const int row = blockIdx.x;  // b * hq + h
+  const int b = row / hq;
+  const int lane = threadIdx.x;
+  // every split row below `splits` is in bounds: read them all while the
+  // sequence length is still on its way, use the first nvalid
+  const float* lse = part_lse + (int64_t)row * splits;
+  const float* po = part_o + (int64_t)row * splits * kHeadDim + 2 * lane;
+  float ls[S];
+  float2 pv[S];
+#pragma unroll
+  for (int sp = 0; sp < S; ++sp) {
+    ls[sp] = sp < splits ? lse[sp] : -INFINITY;
+    pv[sp] = sp < splits ? *reinterpret_cast<const float2*>(po + (int64_t)sp * kHeadDim)
+                         : float2{0.0f, 0.0f};
+  }
+  const int L = min(seqlens[b], max_tokens);
+  const int nvalid = L <= 0 ? 0 : min(splits, (L + split_tokens - 1) / split_tokens);
+  if (nvalid == 1) return;
+  float M = -INFINITY;
+#pragma unroll
+  for (int sp = 0; sp < S; ++sp)
+    if (sp < nvalid) M = fmaxf(M, ls[sp]);
+  float o0 = 0.0f, o1 = 0.0f, den = 0.0f;
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int sp = 0; sp < S; ++sp) {
+      if (sp >= nvalid) break;
+      const float w = exp2_fast(ls[sp] - M);
+      o0 += w * pv[sp].x;
+      o1 += w * pv[sp].y;
+      den += w;
+    }
+  }
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  const uint32_t pk = (uint32_t)Act<T>::from_f32(o0 * inv) |
+                      ((uint32_t)Act<T>::from_f32(o1 * inv) << 16);
+  *reinterpret_cast<uint32_t*>(out + (int64_t)row * kHeadDim + 2 * lane) = pk;
+}
+
 // The same merge for many splits (long contexts): one 1024-thread workgroup
 // per (b, h) row.  Every thread reads lse values for the maximum; wave w then
 // accumulates splits w, w + 16, ... (eight partial rows in flight per lane)
@@ -440,6 +491,10 @@ static hipError_t launch_decode(const DecodeArgs& a, int batch,
     hipLaunchKernelGGL(decode_combine_wide_kernel<T>, dim3((unsigned)(batch * a.hq)),
                        dim3(64 * kWideWaves), 0, stream, a.part_o, a.part_lse, a.seqlens, a.out,
                        a.hq, a.splits, a.pages_per_split * a.bs, a.w * a.bs);
+  else if (a.splits <= 8)
+    hipLaunchKernelGGL((decode_combine_small_kernel<T, 8>), dim3((unsigned)(batch * a.hq)),
+                       dim3(64), 0, stream, a.part_o, a.part_lse, a.seqlens, a.out, a.hq,
+                       a.splits, a.pages_per_split * a.bs, a.w * a.bs);
   else
     hipLaunchKernelGGL(decode_combine_kernel<T>, dim3((unsigned)(batch * a.hq)), dim3(64), 0,
                        stream, a.part_o, a.part_lse, a.seqlens, a.out, a.hq, a.splits,
