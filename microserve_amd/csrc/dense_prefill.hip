@@ -10,9 +10,11 @@
 //
 // MI355X design (the paged FP8 prefill's structure with 16-bit operands):
 //  * A workgroup is four waves over one (sequence, kv head, block of query
-//    tokens); each wave owns two 16-row blocks, a row being one (query
+//    tokens); each wave owns three 16-row blocks, a row being one (query
 //    token, q head) pair of the kv head's GQA group, so every K/V operand
-//    read from LDS feeds two MFMAs.
+//    read from LDS feeds three MFMAs (236 VGPRs: two waves per SIMD, as the
+//    64 KB of LDS per workgroup allows; three blocks measured 6.7% faster
+//    than two).
 //  * K/V tiles of 64 keys (256-byte rows) are staged in LDS with direct
 //    global -> LDS loads, double-buffered in separately declared buffers
 //    with one barrier per tile.  Each row's 16-byte chunks are XOR-swizzled
@@ -42,7 +44,7 @@ namespace mskv {
 
 constexpr int kDStep = 64;  // keys per tile
 constexpr int kDWaves = 4;
-constexpr int kDBlocks = 2;  // 16-row blocks per wave
+constexpr int kDBlocks = 3;  // 16-row blocks per wave
 constexpr int kDThreads = 64 * kDWaves;
 constexpr int kDRow = 2 * kHeadDim;  // bytes per K/V row
 constexpr int kDTile = kDStep * kDRow;
