@@ -90,6 +90,17 @@ def act_dtype(t) -> int:
     raise AssertionError(f"activation dtype must be float16 or bfloat16, got {t.dtype}")
 
 
+def on_device(what: str, ref, *tensors) -> None:
+    """Every tensor argument must live on ``ref``'s GPU: a kernel handed a
+    host pointer faults instead of raising, so mixed placement is rejected
+    here (AssertionError, like the reference's argument checks)."""
+    assert ref.is_cuda, f"{what} runs on the GPU"
+    for t in tensors:
+        if t is not None:
+            assert t.device == ref.device, (
+                f"{what}: every tensor must be on {ref.device}, got one on {t.device}")
+
+
 def stream_of(t) -> int:
     import torch
     return torch.cuda.current_stream(t.device).cuda_stream

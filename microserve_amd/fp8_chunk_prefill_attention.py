@@ -19,7 +19,8 @@ def _check_common(query, k_cache, v_cache, k_scale_cache, v_scale_cache):
     assert head_dim == k_cache.shape[3]
     for t in (k_cache, v_cache, k_scale_cache, v_scale_cache):
         assert t.is_contiguous(), "caches must be contiguous"
-    assert query.is_cuda, "prefill attention runs on the GPU"
+    _lib.on_device("prefill attention", query, k_cache, v_cache, k_scale_cache,
+                   v_scale_cache)
 
 
 def fp8_chunk_prefill_attention(
@@ -42,6 +43,7 @@ def fp8_chunk_prefill_attention(
     query_len, num_q_heads, head_dim = query.shape
     _check_common(query, k_cache, v_cache, k_scale_cache, v_scale_cache)
     assert block_table.dtype == torch.int32
+    _lib.on_device("fp8_chunk_prefill_attention", query, block_table)
     prefix_len = int(prefix_len)
     assert prefix_len >= 0
     output = torch.empty_like(query)
@@ -85,6 +87,8 @@ def fp8_varlen_prefill_attention(
     num_seqs = cu_seqlens_q.numel() - 1
     assert cu_seqlens_k.numel() == num_seqs + 1
     assert block_tables.dim() == 2 and block_tables.shape[0] == num_seqs
+    _lib.on_device("fp8_varlen_prefill_attention", query, block_tables, cu_seqlens_q,
+                   cu_seqlens_k)
     output = torch.empty_like(query)
     if total_q == 0 or num_seqs == 0:
         return output

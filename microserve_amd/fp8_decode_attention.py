@@ -84,7 +84,8 @@ def fp8_decode_attention(
     assert block_tables.shape[0] == batch_size == cache_seqlens.numel()
     for t in (k_cache, v_cache, k_scale_cache, v_scale_cache):
         assert t.is_contiguous(), "caches must be contiguous"
-    assert query.is_cuda, "fp8_decode_attention runs on the GPU"
+    _lib.on_device("fp8_decode_attention", query, k_cache, v_cache, k_scale_cache,
+                   v_scale_cache, cache_seqlens, block_tables, out)
     if out is None:
         out = torch.empty_like(query)
     else:

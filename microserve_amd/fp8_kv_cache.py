@@ -40,7 +40,8 @@ def store_fp8_kvcache(
     assert slot_mapping.numel() == num_tokens
     for t in (k_cache, v_cache, k_scale_cache, v_scale_cache):
         assert t.is_contiguous(), "caches must be contiguous"
-    assert key.is_cuda, "store_fp8_kvcache runs on the GPU"
+    _lib.on_device("store_fp8_kvcache", key, value, k_cache, v_cache, k_scale_cache,
+                   v_scale_cache, slot_mapping)
     num_slots = k_cache.shape[0] * k_cache.shape[1]
     lib = _lib.load()
     status = lib.mskv_store_fp8_kvcache(

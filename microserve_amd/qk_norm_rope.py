@@ -64,6 +64,8 @@ def qk_norm_rope_store(positions, q, k, v, q_norm_weight, k_norm_weight, eps,
     assert k_cache.dtype == torch.float8_e4m3fn and v_cache.dtype == torch.float8_e4m3fn
     assert k_cache.shape[2:] == (hk, d) and v_cache.shape == k_cache.shape
     assert k_scale_cache.shape == k_cache.shape[:-1] and v_scale_cache.shape == k_cache.shape[:-1]
+    _lib.on_device("qk_norm_rope_store", q, k, v, positions, q_norm_weight, k_norm_weight,
+                   cos, sin, k_cache, v_cache, k_scale_cache, v_scale_cache, slot_mapping)
     q_out = torch.empty(n, hq, d, dtype=q.dtype, device=q.device)
     k_out = torch.empty(n, hk, d, dtype=q.dtype, device=q.device) if return_k else None
     lib = _lib.load()

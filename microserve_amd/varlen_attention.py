@@ -44,7 +44,7 @@ def varlen_attention(
     assert cu_seqlens_q.dtype == cu_seqlens_k.dtype == torch.int32
     num_seqs = cu_seqlens_q.numel() - 1
     assert cu_seqlens_k.numel() == num_seqs + 1
-    assert q.is_cuda, "varlen_attention runs on the GPU"
+    _lib.on_device("varlen_attention", q, k, v, cu_seqlens_q, cu_seqlens_k)
     if softmax_scale is None:
         softmax_scale = head_dim ** -0.5
     out = torch.empty_like(q)

@@ -100,3 +100,13 @@ def test_python_wrappers_reject_like_the_reference():
     with pytest.raises(AssertionError):       # int64 lengths
         fp8_decode_attention(q.bfloat16(), kc, kc, ks, ks, torch.ones(2, dtype=torch.int64),
                              torch.zeros(2, 1, dtype=torch.int32), 0.1)
+
+
+def test_wrappers_reject_tensors_off_the_gpu():
+    """A host tensor among GPU arguments is rejected before any launch (a
+    kernel given a host pointer would fault).  Checked with CPU tensors only:
+    the first check (the reference tensor on the GPU) already fails here."""
+    import torch
+    from microserve_amd import _lib as L
+    with pytest.raises(AssertionError, match="runs on the GPU"):
+        L.on_device("x", torch.zeros(1))

@@ -114,3 +114,26 @@ def test_attention_unknown_mode_raises():
                  torch.zeros(1, 8, H.D, dtype=torch.bfloat16, device=H.DEV))
     finally:
         reset_context()
+
+
+@pytest.mark.gpu
+def test_wrappers_reject_host_tensors_among_gpu_arguments():
+    """A host tensor among GPU arguments raises before any launch."""
+    from microserve_amd import (fp8_decode_attention, qk_norm_rope_store, store_fp8_kvcache,
+                                varlen_attention)
+    from tests.gpu_helpers import alloc_cache
+    kc, vc, ks, vs = alloc_cache(2)
+    key = torch.zeros(3, 8, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(AssertionError, match="must be on"):
+        store_fp8_kvcache(key, key, kc, vc, ks, vs, torch.zeros(3, dtype=torch.int64))
+    q = torch.zeros(3, 32, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(AssertionError, match="must be on"):
+        fp8_decode_attention(q, kc, vc, ks, vs, torch.ones(3, dtype=torch.int32, device="cuda"),
+                             torch.zeros(3, 1, dtype=torch.int32), 0.1)
+    cu = torch.tensor([0, 3], dtype=torch.int32)
+    with pytest.raises(AssertionError, match="must be on"):
+        varlen_attention(q, key, key, cu, cu.cuda(), 3, 3, 0.1)
+    tab = torch.ones(16, 128, dtype=torch.bfloat16, device="cuda")
+    with pytest.raises(AssertionError, match="must be on"):
+        qk_norm_rope_store(torch.zeros(3, dtype=torch.int64), q, key, key, None, None, 1e-6, tab,
+                           tab, kc, vc, ks, vs, torch.zeros(3, dtype=torch.int64, device="cuda"))
