@@ -15,6 +15,9 @@ plus queries, outputs, tables and lengths), ``roofline`` compares the decode
 op (split-KV kernel + combine) with the 8 TB/s HBM peak, ``store`` reports
 store_kvcache tokens/s on the 262,144-token pool fill, and ``cpu_baseline``
 times the oracle's torch-CPU decode on a bounded sample of the same workload.
+The other objects (prefill, fresh prefill, ragged and long-context decode,
+the step-input builder, the fused norm + rotary + store) are measured in the
+same run; the last two carry CPU baselines of their own from the oracle.
 """
 
 from __future__ import annotations
@@ -419,6 +422,15 @@ def _wall_us(fn, iters):
     return statistics.median(times)
 
 
+def _cpu_step_inputs(seqs):
+    """The oracle's restatement of the runner's decode builder on the host
+    (host arrays, no device copies): microseconds for one step."""
+    from oracle import step_inputs_oracle as SO
+    t0 = time.perf_counter()
+    SO.compile_decode(seqs, BS)
+    return (time.perf_counter() - t0) * 1e6
+
+
 def time_step_inputs(dev, iters=30):
     """Per-step input building: the device builder (one pinned copy + one
     step_inputs_kernel launch) against the runner's element-by-element device
@@ -449,11 +461,16 @@ def time_step_inputs(dev, iters=30):
     _elementwise_prefill_inputs(sample, dev)
     ref_sample_us = _wall_us(lambda: _elementwise_prefill_inputs(sample, dev), 3)
     ref_pre_us = ref_sample_us * FRESH_LEN / 256
+    cpu_dec_us = _cpu_step_inputs(seqs)
     return {"decode": {"workload": "decode step, batch 256, context log-uniform on "
                                    "[16, 32768], block 256, 40k-block pool",
                        "us": round(dec_us, 1), "graph_padded_us": round(graph_us, 1),
                        "elementwise_us": round(ref_dec_us, 1),
-                       "speedup": round(ref_dec_us / dec_us, 1)},
+                       "speedup": round(ref_dec_us / dec_us, 1),
+                       "cpu_baseline": {"value": round(cpu_dec_us, 1), "unit": "us", "cores": 1,
+                                        "kind": "port",
+                                        "sample": "the oracle's loops building the same step "
+                                                  "into host arrays (no device copies)"}},
             "prefill": {"workload": "fresh prefill step, 8 prompts x 8192 tokens, block 256",
                         "us": round(pre_us, 1),
                         "elementwise_us": round(ref_pre_us, 1),
@@ -539,13 +556,41 @@ def time_norm_rope(dev, iters=20, warmup=3):
             torch.cuda.synchronize()
             res[name] = e0.elapsed_time(e1) / iters * 1e3
         nbytes = norm_rope_bytes(n, HQ, HK, with_k)
+        cpu = _cpu_norm_rope(qkv, pos, qw, kw, cos_t, sin_t, slots, nb) if mode == "prefill" else None
         out.append({"workload": f"{mode}: {n} tokens, 32 q / 8 kv heads, bf16, rotary table "
                                 f"40960 x 128",
                     "us": round(res["fused"], 2), "unfused_us": round(res["unfused"], 2),
                     "speedup": round(res["unfused"] / res["fused"], 2),
                     "bytes": nbytes, "gbs": round(nbytes / res["fused"] / 1e3, 1),
-                    "frac": round(nbytes / res["fused"] / 1e3 / HBM_PEAK_GBS, 4)})
+                    "frac": round(nbytes / res["fused"] / 1e3 / HBM_PEAK_GBS, 4),
+                    **({"cpu_baseline": cpu} if cpu else {})})
     return out
+
+
+def _cpu_norm_rope(qkv, pos, qw, kw, cos_t, sin_t, slots, nb, sample=4096):
+    """The oracle's norm + rotary + FP8 store on the host cores, on the first
+    ``sample`` tokens of the same step (a bounded sample)."""
+    import numpy as np
+    from oracle import fp8_oracle as O
+    from oracle import norm_rope_oracle as NR
+    torch.set_num_threads(os.cpu_count() or 1)
+    x = qkv[:sample].cpu()
+    p = pos[:sample].cpu()
+    q, k, v = (t.view(sample, -1, D) for t in x.split([HQ * D, HK * D, HK * D], dim=-1))
+    c, s_ = cos_t.cpu(), sin_t.cpu()
+    w_q, w_k = qw.cpu(), kw.cpu()
+    sl = slots[:sample].cpu().numpy()
+    kc = np.zeros((nb, BS, HK, D), np.uint8)
+    vc = np.zeros_like(kc)
+    ks = np.ones((nb, BS, HK), np.float32)
+    vs = np.ones_like(ks)
+    t0 = time.perf_counter()
+    _, rk = NR.qk_norm_rope(q, k, p, w_q, w_k, 1e-6, c, s_)
+    O.store_fp8_kvcache(rk.float().numpy(), v.float().numpy(), kc, vc, ks, vs, sl)
+    dt = time.perf_counter() - t0
+    return {"value": round(sample / dt, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port", "sample": f"{sample} tokens of the prefill step, oracle in numpy/torch "
+                                      f"on the host"}
 
 
 def _rope_tables_bf16(max_position, base=1e6):
