@@ -35,10 +35,12 @@
 //  * Tiles are double-buffered in LDS: step i+1's rows are staged while
 //    step i is consumed, so the K/V registers live only while in flight.
 //  * Split-KV: the host picks pages-per-split from shapes only; each split
-//    writes (o / l, m + log2 l) partials and decode_combine_kernel merges
-//    them (an in-kernel merge needs agent-scope fences, i.e. an L2
-//    writeback + invalidate per XCD, which measured 2x slower).  A sequence
-//    that fits in one split is written directly by the split kernel.
+//    writes (o / l, m + log2 l) partials and a second kernel merges them:
+//    decode_combine_small_kernel up to 8 splits, decode_combine_kernel up
+//    to 64, decode_combine_wide_kernel beyond (an in-kernel merge needs
+//    agent-scope fences, i.e. an L2 writeback + invalidate per XCD, which
+//    measured 2x slower).  A sequence that fits in one split is written
+//    directly by the split kernel.
 //  * Every page is read through a buffer resource sized to that page; an
 //    invalid block id gives a zero-length resource (loads return 0) and its
 //    tokens are masked, so a bad table entry cannot fault.
