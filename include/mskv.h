@@ -126,7 +126,9 @@ int mskv_fp8_decode_attention(const void* query, const void* k_cache,
  * query is split into e4m3 parts under a power-of-two row scale, and the
  * probabilities into hi + lo parts under a per-row E8M0 block scale.
  * query/out: [total_q, num_q_heads, head_dim] in act_dtype; block_tables:
- * int32 [num_seqs, max_blocks_per_seq].
+ * int32 [num_seqs, max_blocks_per_seq].  max_seqlen_q must be at least
+ * every sequence's query count: it sizes the grid, and query rows past it
+ * are not written (flash-attn's contract for the same argument).
  * Supported: head_dim == 128, block_size % 128 == 0, GQA group <= 16 or a
  * multiple of 16.
  */
@@ -157,6 +159,8 @@ int mskv_fp8_prefill_attention(const void* query, const void* k_cache,
  * fp32 accumulation; the probabilities are rounded to act_dtype.
  * query/out: [total_q, num_q_heads, head_dim]; key/value:
  * [total_k, num_kv_heads, head_dim], all contiguous in act_dtype.
+ * max_seqlen_q must be at least every sequence's query count: it sizes the
+ * grid, and query rows past it are not written (as in flash-attn).
  * Supported: head_dim == 128, GQA group <= 16 or a multiple of 16.
  */
 int mskv_prefill_attention(const void* query, const void* key,
