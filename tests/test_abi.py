@@ -83,6 +83,36 @@ def test_argument_validation_without_launch():
     assert lib.mskv_fp8_prefill_attention(1, 1, 1, 1, 1, 1, None, None, 0, 1, 1, 10, 10, 32, 8, 128, 64, 10, 4, 0.1, 1, None) == EUNSUP
 
 
+def test_new_entry_points_validate_without_launch():
+    lib = _lib.load()
+    EINVAL, EUNSUP = -1, -2
+    A = 1 << 20  # a 16-byte aligned stand-in address; nothing is launched
+    # fused prologue: args before (q, k, v, strides, positions, weights, eps, cos, sin, maxpos)
+    def nr(head_dim=128, qw=A, kw=A, q=A, qs=48 * 128, n=4, eps=1e-6, slot_dtype=1, act=1):
+        return lib.mskv_qk_norm_rope_store(
+            q, A, A, qs, 48 * 128, 48 * 128, A, qw, kw, eps, A, A, 4096, A, None, A, A, A, A, A,
+            slot_dtype, n, 32, 8, head_dim, 1 << 16, act, None)
+    assert nr(head_dim=64) == EUNSUP
+    assert nr(kw=None) == EINVAL            # one weight without the other
+    assert nr(q=A + 8) == EINVAL            # q not 16-byte aligned
+    assert nr(qs=32 * 128 - 8) == EINVAL    # token stride shorter than the q heads
+    assert nr(eps=-1.0) == EINVAL
+    assert nr(slot_dtype=5) == EINVAL
+    assert nr(act=3) == EINVAL
+    assert nr(n=0) == 0                     # nothing to do
+    # step inputs: (token_ids, starts, cu_q, table_off, tables, num_seqs, pad_seqs, total_q,
+    #               block_size, table_width, garbage, ids, pos, slot, lens, tables_out, max_q)
+    def si(num_seqs=2, pad=2, total_q=3, bs=256, width=4, ids=A, max_q=2):
+        return lib.mskv_build_step_inputs(A, A, A, A, A, num_seqs, pad, total_q, bs, width, 0,
+                                          ids, A, A, A, A, max_q, None)
+    assert si(pad=1) == EINVAL              # fewer padded rows than sequences
+    assert si(bs=0) == EINVAL
+    assert si(width=-1) == EINVAL
+    assert si(ids=None) == EINVAL           # rows to write but no output
+    assert si(num_seqs=70000, pad=70000) == EUNSUP  # grid y limit
+    assert si(num_seqs=0, pad=0, total_q=0) == 0
+
+
 def test_python_wrappers_reject_like_the_reference():
     torch = pytest.importorskip("torch")
     from microserve_amd import fp8_decode_attention, store_fp8_kvcache
