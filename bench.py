@@ -120,10 +120,24 @@ def cpu_baseline(w, budget_s=10.0):
         t_total += time.perf_counter() - t0
         done += 1
     gbs = decode_bytes(done, CTX, HQ, HK, D) / t_total / 1e9
+    # the store on the host: the oracle quantizing and scattering a bounded
+    # sample of the fill's tokens (the first 16,384 of them)
+    key, value, slots = (t[:16384].cpu() for t in w["fills"][0])
+    skc = np.zeros(tuple(w["kc"].shape), np.uint8)
+    svc = np.zeros_like(skc)
+    sks = np.ones(tuple(w["ks"].shape), np.float32)
+    svs = np.ones_like(sks)
+    t0 = time.perf_counter()
+    O.store_fp8_kvcache(key.float().numpy(), value.float().numpy(), skc, svc, sks, svs,
+                        slots.numpy())
+    store_s = time.perf_counter() - t0
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "os_cpu_count": os.cpu_count(), "kind": "port",
             "sample": f"{done} single-sequence decodes (4096 tokens, 32 q / 8 kv heads) "
-                      f"cycling over the Qwen3-8B batch, torch fp32 oracle, {t_total:.1f} s"}
+                      f"cycling over the Qwen3-8B batch, torch fp32 oracle, {t_total:.1f} s",
+            "store": {"value": round(key.shape[0] / store_s, 1), "unit": "tokens/s",
+                      "sample": f"{key.shape[0]} tokens of the 262,144-token fill, numpy "
+                                f"oracle, {store_s:.2f} s"}}
 
 
 PRE_SEQS, PRE_CACHED, PRE_NEW = 8, 8192, 2048
