@@ -11,14 +11,21 @@ from microserve_amd import _lib
 
 # Per device, the split-partials scratch, grown on demand and reused by
 # every call: decode calls on one stream (graph replays included) run one
-# after another, so they never hold it at the same time.
+# after another, so they never hold it at the same time.  A graph captured
+# before the scratch grew still addresses the old buffer, so a grown-out
+# buffer is retired, never freed; growth at least doubles, so few exist.
 _SCRATCH: dict = {}
+_RETIRED: list = []
 
 
 def _scratch(device: torch.device, nbytes: int) -> torch.Tensor:
     buf = _SCRATCH.get(device)
     if buf is None or buf.numel() < nbytes:
-        buf = torch.empty(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        size = max(nbytes, 1 << 16)
+        if buf is not None:
+            _RETIRED.append(buf)
+            size = max(size, 2 * buf.numel())
+        buf = torch.empty(size, dtype=torch.uint8, device=device)
         _SCRATCH[device] = buf
     return buf
 

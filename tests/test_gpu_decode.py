@@ -3,6 +3,7 @@
 1e-2 relative (Frobenius) error, plus size-independent properties at the
 Qwen3-8B / 32B shapes."""
 
+import importlib
 import os
 import sys
 
@@ -254,3 +255,52 @@ def test_decode_scratch_reuse_across_shapes():
     torch.cuda.synchronize()
     assert torch.equal(a, c)
     assert (small.float() - a[:8].float()).abs().max().item() < 1e-2
+
+
+def test_decode_graph_survives_scratch_growth(monkeypatch):
+    """A graph captured before a larger batch grew the partials scratch still
+    replays correctly: the buffer it addresses is kept, not handed back to
+    the allocator for other tensors (the runner captures its graphs from the
+    smallest batch up, with an eager warm-up of each before capture)."""
+    M = importlib.import_module("microserve_amd.fp8_decode_attention")
+    monkeypatch.setattr(M, "_SCRATCH", {})
+    monkeypatch.setattr(M, "_RETIRED", [])
+    lens = [4096] * 64
+    query, tables, caches = _setup(141, lens, 32, 8, 1100)
+    q = query.to(H.DEV)
+    t = tables.to(H.DEV)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=H.DEV)
+    small = dict(q=q[:1].clone(), lens=lens_d[:1].clone(), t=t[:1].clone(),
+                 out=torch.zeros_like(q[:1]))
+
+    def step():
+        fp8_decode_attention(small["q"], *caches, small["lens"], small["t"], 0.088,
+                             out=small["out"])
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    captured = M._SCRATCH[q.device]
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    want = fp8_decode_attention(q, *caches, lens_d, t, 0.088)
+    torch.cuda.synchronize()
+    assert M._SCRATCH[q.device] is not captured, "the large batch must grow the scratch"
+    assert any(r is captured for r in M._RETIRED)
+    # tensors of the old buffer's size, filled with a pattern: a freed
+    # buffer would be handed to one of them and the replay would overwrite it
+    churn = [torch.full((captured.numel(),), 0x5A, dtype=torch.uint8, device=H.DEV)
+             for _ in range(4)]
+    graph.replay()
+    torch.cuda.synchronize()
+    got = small["out"].clone()
+    eager = fp8_decode_attention(small["q"], *caches, small["lens"], small["t"], 0.088)
+    torch.cuda.synchronize()
+    assert torch.equal(got, eager)
+    assert (got.float() - want[:1].float()).abs().max().item() < 1e-2
+    for c in churn:
+        assert bool((c == 0x5A).all()), "the replay wrote into another tensor"
