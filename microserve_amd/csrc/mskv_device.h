@@ -125,7 +125,10 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
 // must already lie in [-448, 448].
 __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c,
                                                float d) {
-  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  // the first convert keeps the high half of its old value and the second
+  // overwrites it: passing a's bits as that old value, rather than 0, lets
+  // the result take a's register without a move
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, __float_as_int(a), false);
   w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
   return (uint32_t)w;
 }

@@ -124,6 +124,8 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
   __shared__ __attribute__((aligned(16))) uint8_t v_lds1[kPStep * kHeadDim];
   __shared__ __attribute__((aligned(16))) float sc_lds0[2][kPStep];
   __shared__ __attribute__((aligned(16))) float sc_lds1[2][kPStep];
+  // each wave's reciprocals of the current tile's v_scales
+  __shared__ __attribute__((aligned(16))) float rv_lds[kPWaves][kPStep];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -395,15 +397,25 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
         m_use[b] = (m[b] == -INFINITY ? 0.0f : m[b]) - lf - kf;
         lsum[b] = 0.0f;
       }
+      // 1 / v_scale of the tile's keys, computed once per key by this wave
+      // (lane i: keys i and 64 + i) instead of once per lane group, and read
+      // back below like the scales.  v_scale is 0 only for keys past
+      // `valid`, whose weights are 0.  The wave reads back only its own
+      // writes, so a wave-level barrier orders them.
+      float* rvw = rv_lds[wave];
+      {
+        const float v0 = vss[lane], v1 = vss[64 + lane];
+        rvw[lane] = v0 > 0.0f ? __builtin_amdgcn_rcpf(v0) : 0.0f;
+        rvw[64 + lane] = v1 > 0.0f ? __builtin_amdgcn_rcpf(v1) : 0.0f;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
       typedef float f32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
       for (int tt = 0; tt < 8; ++tt) {
         const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
-        // v_scale is 0 only for keys past `valid`, whose weights are 0
-        f32x4 rv;
-#pragma unroll
-        for (int r = 0; r < 4; ++r)
-          rv[r] = full || vsc[r] > 0.0f ? __builtin_amdgcn_rcpf(vsc[r]) : 0.0f;
+        const f32x4 rv = *reinterpret_cast<const f32x4*>(rvw + 16 * tt + 4 * g);
 #pragma unroll
         for (int b = 0; b < kPBlocks; ++b) {
           float y[4];
