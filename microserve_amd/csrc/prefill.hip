@@ -58,6 +58,10 @@ constexpr float kPSlack = 8.0f;
 // The tile's v_scales are scaled by a power of two to at most this value, so
 // p * v_scale (p <= 1 after the per-row normalization) stays within 448.
 constexpr float kPVScaleMax = 384.0f;
+// Below this v_scale * fcur the two e4m3 parts of a key's weight
+// p * v_scale * fcur (at most 1/4 for such a key) hold too few bits for
+// its share of the softmax denominator, so its exact p goes there instead.
+constexpr float kPTinyV = 0.25f;
 
 // e4m3 parts the query is split into: a bf16 value has 8 significant bits
 template <typename T> struct QuerySplit { static constexpr int parts = 3; };
@@ -402,14 +406,43 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
       // back below like the scales.  v_scale is 0 only for keys past
       // `valid`, whose weights are 0.  The wave reads back only its own
       // writes, so a wave-level barrier orders them.
+      // A key whose v_scale * fcur is below kPTinyV (V amax under ~1/1500 of
+      // the tile's largest, e.g. a V row stored as zeros) would get weights
+      // p * v_scale too small for e4m3 to carry, and its probability would
+      // drop out of l.  Its reciprocal is 0 instead, and its exact weight
+      // joins l on the rare path below.  Its V contribution stays with the
+      // MFMA, which it changes by at most p / 1500 of the tile's largest |V|.
       float* rvw = rv_lds[wave];
+      bool tiny_keys;
       {
         const float v0 = vss[lane], v1 = vss[64 + lane];
-        rvw[lane] = v0 > 0.0f ? __builtin_amdgcn_rcpf(v0) : 0.0f;
-        rvw[64 + lane] = v1 > 0.0f ? __builtin_amdgcn_rcpf(v1) : 0.0f;
+        const bool t0 = v0 > 0.0f && v0 * fcur < kPTinyV;
+        const bool t1 = v1 > 0.0f && v1 * fcur < kPTinyV;
+        rvw[lane] = v0 > 0.0f && !t0 ? __builtin_amdgcn_rcpf(v0) : 0.0f;
+        rvw[64 + lane] = v1 > 0.0f && !t1 ? __builtin_amdgcn_rcpf(v1) : 0.0f;
+        tiny_keys = __any(t0 || t1);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      }
+      if (tiny_keys) {
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) {
+          const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            if (vsc[r] > 0.0f && vsc[r] * fcur < kPTinyV) {
+#pragma unroll
+              for (int b = 0; b < kPBlocks; ++b) {
+                // opaque to the optimizer: shared with the loop below, these
+                // exps would be hoisted out of the loop's MFMA interleave
+                float x = fmaf(st[b][tt][r], qs[b], -m_use[b]);
+                asm volatile("" : "+v"(x));
+                lsum[b] += exp2_fast(x);
+              }
+            }
+          }
+        }
       }
       typedef float f32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll

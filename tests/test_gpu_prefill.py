@@ -96,6 +96,38 @@ def test_varlen_prefill_qwen3_8b_chunk_with_outliers():
     print(f"outlier chunk prefill: max_abs {max_abs:.4e} rel {rel:.4e}")
 
 
+@pytest.mark.parametrize("v_mult", [0.0, 1e-6])
+def test_varlen_prefill_dominant_keys_with_vanishing_values(v_mult):
+    """5% of the keys take ~95% of the attention, and their V rows are zero
+    (stored with the 1e-8 / 448 floor scale) or 1e-6 of the others.  Their
+    probability still counts in the softmax denominator, as in the
+    reference, so the output stays near zero instead of becoming the
+    average of the remaining keys."""
+    gen = torch.Generator().manual_seed(241)
+    hq, hk = 32, 8
+    lq = [48, 96]
+    lk = [700 + 48, 300 + 96]
+    nb = sum((n + 255) // 256 for n in lk) + 2
+    tables, slots = H.paged_layout(gen, lk, nb)
+    n = slots.numel()
+    key = torch.randn(n, hk, H.D, generator=gen)
+    value = torch.randn(n, hk, H.D, generator=gen)
+    u = torch.randn(hk, H.D, generator=gen)
+    u = u / u.norm(dim=-1, keepdim=True)
+    special = torch.rand(n, generator=gen) < 0.05
+    key[special] = 19.0 * u  # logit ~5 above the others (softmax scale 1/sqrt(128))
+    value[special] = value[special] * v_mult
+    query = torch.randn(sum(lq), hq, H.D, generator=gen)
+    query = query + 3.0 * u.repeat_interleave(hq // hk, dim=0)[None]
+    key, value, query = key.bfloat16(), value.bfloat16(), query.bfloat16()
+    caches = H.alloc_cache(nb, H.BLOCK, hk)
+    store_fp8_kvcache(key.to(H.DEV), value.to(H.DEV), *caches, slots.to(H.DEV))
+    cu_q = torch.tensor([0] + list(np.cumsum(lq)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(lk)), dtype=torch.int32)
+    max_abs, rel = _varlen_check(query, tables, caches, cu_q, cu_k, lq)
+    print(f"vanishing-V dominant keys (x{v_mult}): max_abs {max_abs:.4e} rel {rel:.4e}")
+
+
 def test_chunk_prefill_single_equals_varlen():
     lq, lk = [100], [100 + 700]
     query, tables, caches, cu_q, cu_k = _varlen_setup(231, lq, lk, 32, 8)
