@@ -26,8 +26,9 @@
 //    out of the V tile transposed with ds_read_b64_tr_b8, then is converted
 //    fp8 -> bf16 in registers.
 //  * Tile rows are stored with their 16-byte chunks XOR-swizzled by
-//    (row / 2) % 8, which makes the row-major writes, the K reads and the
-//    transposed V reads all free of LDS bank conflicts.
+//    (row / 2) % 8, which keeps the row-major writes and the K reads free
+//    of LDS bank conflicts; the transposed V reads are 2-way (rows r and
+//    r + 16 share banks), which this HBM-bound kernel does not feel.
 //  * Online softmax in base 2 (v_exp_f32); the row max is a two-step xor
 //    reduction (v_permlane16/32_swap, no LDS round trip) across the four
 //    lane groups that share a head, and the accumulator is rescaled lazily,

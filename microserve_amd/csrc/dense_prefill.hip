@@ -18,8 +18,9 @@
 //  * K/V tiles of 64 keys (256-byte rows) are staged in LDS with direct
 //    global -> LDS loads, double-buffered in separately declared buffers
 //    with one barrier per tile.  Each row's 16-byte chunks are XOR-swizzled
-//    by row % 16, which keeps the K operand reads (one chunk of 16 rows) and
-//    the transposed V reads (two chunks of 16 rows) free of bank conflicts.
+//    by row % 16, which keeps the K operand reads (one chunk of 16 rows)
+//    free of bank conflicts and leaves the transposed V reads 2-way; a
+//    swizzle without those conflicts measured no faster.
 //    The buffer resources end at the last key of the sequence, so rows past
 //    it read as zeros.
 //  * S^T = K . Q^T on v_mfma_f32_16x16x32_{bf16,f16}: lane (g, n) gets keys

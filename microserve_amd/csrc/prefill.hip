@@ -7,16 +7,19 @@
 // block_tables[s][p / BS] * BS + p % BS.
 //
 // MI355X design:
-//  * A workgroup is four waves over one (sequence, kv head, block of query
+//  * A workgroup covers 128 rows of one (sequence, kv head, block of query
 //    tokens).  A row is one (query token, q head) pair; the GQA group of the
 //    kv head fills the rows, so every K/V tile serves all the q heads that
-//    read it.  Each wave owns two 16-row blocks: every K and V operand it
-//    reads from LDS feeds both, which halves LDS traffic per FLOP.
+//    read it.  bf16 runs four waves of two 16-row blocks, so every K and V
+//    operand a wave reads from LDS feeds both, which halves LDS traffic per
+//    FLOP; fp16, whose query needs a third e4m3 part, runs eight waves of
+//    one block to stay within the register file.
 //  * K/V tiles of 128 keys (one f8f6f4 MFMA contraction) are staged in LDS,
 //    double-buffered with one barrier per tile.  Rows are written with their
 //    16-byte chunks XOR-swizzled by (row / 2) % 8, which keeps the row
-//    writes, the K operand reads and the transposed V reads free of bank
-//    conflicts.
+//    writes and the K operand reads free of bank conflicts; the transposed
+//    V reads are 2-way (rows r and r + 16 share banks), and a swizzle that
+//    removes that measured slower.
 //  * QK^T: S^T = K . Q8^T with v_mfma_f32_16x16x128_f8f6f4 -- the whole
 //    head_dim is one MFMA.  K bytes are used as stored.  The query row is
 //    scaled by a power of two (exact) and split into e4m3 parts: hi + lo
@@ -28,8 +31,13 @@
 //    ds_read_b64_tr_b8.  P * v_scale is split into e4m3 hi + lo parts after
 //    a per-tile power-of-two scale chosen from the tile's largest v_scale;
 //    the accumulator is rescaled (exactly) only when that power changes.
+//  * The softmax denominator sums the weights the MFMA applies,
+//    (hi + lo) / v_scale, so each output is an exact convex combination of
+//    V rows.  Each wave computes the tile's 1 / v_scale once per key into
+//    LDS; keys whose V is too small for their weights to fit e4m3 add their
+//    exact p on a rare wave-uniform path instead.
 //  * Online softmax in base 2 with a lazy rescale: the accumulator is
-//    rescaled only when some row's max grows by more than 2^2.  Masks are
+//    rescaled only when some row's max grows by more than 2^8.  Masks are
 //    evaluated only on tiles that straddle the causal diagonal or the end
 //    of the keys; fully visible tiles skip them.
 //  * Query blocks are launched last-first, so the longest workgroups start
