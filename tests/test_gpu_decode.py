@@ -114,6 +114,16 @@ def test_decode_invalid_block_ids_read_as_empty():
     H.assert_attention_close(out[1:], ref1)
 
 
+@pytest.mark.parametrize("block_size", [512, 1024])
+def test_decode_larger_block_sizes(block_size):
+    """Pages of 512 and 1024 tokens (any multiple of 256 is a valid
+    block_size, Config.py:28): lengths around page boundaries."""
+    lens = [1, 511, 512, 513, 1500, 3000, 4096]
+    nb = sum((n + block_size - 1) // block_size for n in lens) + 2
+    query, tables, caches = _setup(151, lens, 32, 8, nb, block_size=block_size)
+    _run_and_check(query, lens, tables, caches)
+
+
 def test_decode_qwen3_8b_full_shape():
     """Batch 64 x 4096 tokens, 32 q / 8 kv heads, 2048-block permuted pool."""
     lens = [4096] * 64

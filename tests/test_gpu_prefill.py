@@ -38,11 +38,11 @@ def test_chunk_prefill_reference_case():
 
 
 def _varlen_setup(seed, lq, lk, hq, hk, dtype=torch.bfloat16, outliers=0.0,
-                  extra_blocks=3):
+                  extra_blocks=3, block_size=H.BLOCK):
     gen = torch.Generator().manual_seed(seed)
-    pages = sum((n + 255) // 256 for n in lk)
+    pages = sum((n + block_size - 1) // block_size for n in lk)
     nb = pages + extra_blocks
-    tables, slots = H.paged_layout(gen, lk, nb)
+    tables, slots = H.paged_layout(gen, lk, nb, block_size)
     n = slots.numel()
     key = torch.randn(n, hk, H.D, generator=gen)
     if outliers:
@@ -51,7 +51,7 @@ def _varlen_setup(seed, lq, lk, hq, hk, dtype=torch.bfloat16, outliers=0.0,
     key = key.to(dtype)
     value = H.randn(gen, (n, hk, H.D), dtype)
     query = H.randn(gen, (sum(lq), hq, H.D), dtype)
-    caches = H.alloc_cache(nb, H.BLOCK, hk)
+    caches = H.alloc_cache(nb, block_size, hk)
     store_fp8_kvcache(key.to(H.DEV), value.to(H.DEV), *caches, slots.to(H.DEV))
     cu_q = torch.tensor([0] + list(np.cumsum(lq)), dtype=torch.int32)
     cu_k = torch.tensor([0] + list(np.cumsum(lk)), dtype=torch.int32)
@@ -83,6 +83,17 @@ def test_varlen_prefill_gqa_groups(hq, hk):
     lq = [64, 130]
     lk = [64 + 300, 130 + 5]
     query, tables, caches, cu_q, cu_k = _varlen_setup(211 + hq, lq, lk, hq, hk)
+    _varlen_check(query, tables, caches, cu_q, cu_k, lq)
+
+
+@pytest.mark.parametrize("block_size", [512, 1024])
+def test_varlen_prefill_larger_block_sizes(block_size):
+    """Pages of 512 and 1024 tokens: 128-key tiles never straddle a page,
+    and prefixes and chunks end mid-page."""
+    lq = [100, 1, 300]
+    lk = [100 + 700, 1 + 1023, 300 + 1100]
+    query, tables, caches, cu_q, cu_k = _varlen_setup(251, lq, lk, 32, 8,
+                                                      block_size=block_size)
     _varlen_check(query, tables, caches, cu_q, cu_k, lq)
 
 
