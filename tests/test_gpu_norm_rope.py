@@ -70,13 +70,16 @@ def test_fused_prologue_matches_oracle(dtype, hq, hk, n):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_fused_store_equals_store_kernel_on_the_rotated_k(dtype):
+def test_fused_store_equals_store_kernel_on_the_rotated_k(dtype, slot_dtype):
     """Composition: the fused store writes the bytes the standalone store
-    kernel writes from the same rotated k."""
+    kernel writes from the same rotated k, with int64 slots and with the
+    int32 slots the runner's warmup passes."""
     from microserve_amd import store_fp8_kvcache
     hq, hk, n = 32, 8, 512
     qkv, pos, slots, qw, kw = _inputs(n, hq, hk, dtype, seed=9)
+    slots = slots.to(slot_dtype)
     cos, sin = NR.rope_tables(MAXPOS, 1e6, dtype)
     q, k, v = _split(qkv.to(DEV), hq, hk)
     a = alloc_cache(64, kv_heads=hk)
