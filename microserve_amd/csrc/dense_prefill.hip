@@ -194,6 +194,9 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
     if (t0 >= w_none) return;
     // S^T = K . Q^T: four 16-key tiles, head_dim in four 32-wide chunks
     f32x4 st[kDBlocks][4];
+    // wave priority 1 over the MFMA bursts: measured 1.2% faster than
+    // leaving both waves of a SIMD at equal priority
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int tt = 0; tt < 4; ++tt) {
 #pragma unroll
@@ -205,6 +208,7 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
           st[b][tt] = A::mfma(ka, qop[b][c], c == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : st[b][tt]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     const bool full = t0 + kDStep <= w_all && t0 + kDStep <= lk;
     if (!full) {
 #pragma unroll
@@ -259,6 +263,7 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
       l[b] += psum;
     }
     // O^T += V^T . P^T, one 16-wide d tile and 32-key chunk per MFMA
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const uint32_t vo = v_row + ((32u * dt) ^ v_x);
@@ -278,6 +283,7 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
         for (int b = 0; b < kDBlocks; ++b) acc[b][dt] = A::mfma(va, pv[b][ch], acc[b][dt]);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   if (kv_end > 0) {
