@@ -52,7 +52,7 @@ def store_bytes(n, hk, d, act_bytes=2, slot_bytes=8):
     return n * (2 * hk * d * act_bytes + 2 * hk * d + 2 * hk * 4 + slot_bytes)
 
 
-def build_workload(dev):
+def build_workload(dev, dtype=torch.bfloat16):
     from microserve_amd import store_fp8_kvcache
     gen = torch.Generator().manual_seed(2024)
     perm = torch.randperm(POOL, generator=gen).to(torch.int32)
@@ -67,11 +67,11 @@ def build_workload(dev):
     fills = []
     for t in tables:
         slots = (t[:, pos // BS].long() * BS + pos % BS).reshape(-1)
-        key = torch.randn(slots.numel(), HK, D, generator=gen).bfloat16()
-        value = torch.randn(slots.numel(), HK, D, generator=gen).bfloat16()
+        key = torch.randn(slots.numel(), HK, D, generator=gen).to(dtype)
+        value = torch.randn(slots.numel(), HK, D, generator=gen).to(dtype)
         fills.append((key.to(dev), value.to(dev), slots.to(dev)))
         store_fp8_kvcache(fills[-1][0], fills[-1][1], kc, vc, ks, vs, fills[-1][2])
-    query = torch.randn(BATCH, HQ, D, generator=gen).bfloat16().to(dev)
+    query = torch.randn(BATCH, HQ, D, generator=gen).to(dtype).to(dev)
     seqlens = torch.full((BATCH,), CTX, dtype=torch.int32, device=dev)
     return dict(kc=kc, vc=vc, ks=ks, vs=vs, query=query, seqlens=seqlens,
                 tables=[t.to(dev) for t in tables], fills=fills)
@@ -97,6 +97,29 @@ def time_store_fill(w, iters=5):
     return {"tokens": n, "tokens_per_s": n / t, "us": t * 1e6,
             "gbs": store_bytes(n, HK, D) / t / 1e9,
             "frac": store_bytes(n, HK, D) / t / 1e9 / HBM_PEAK_GBS}
+
+
+def time_fp16(dev, iters=200, warmup=20):
+    """The headline decode and store fill with fp16 activations, the dtype the
+    reference requires for its FP8 cache (Config.py:35-36)."""
+    from microserve_amd import fp8_decode_attention
+    w = build_workload(dev, torch.float16)
+    torch.cuda.synchronize()
+    out = torch.empty_like(w["query"])
+
+    def step(i):
+        fp8_decode_attention(w["query"], w["kc"], w["vc"], w["ks"], w["vs"],
+                             w["seqlens"], w["tables"][i % 2], D ** -0.5, out=out)
+
+    us = _time_steps(step, iters, warmup)
+    nbytes = decode_bytes(BATCH, CTX, HQ, HK, D)
+    store = time_store_fill(w)
+    return {"workload": "the Qwen3-8B batch 64 x 4096 decode and the 262,144-token store "
+                        "fill, fp16 q/K/V",
+            "decode_us": round(us, 2), "decode_gbs": round(nbytes / us / 1e3, 1),
+            "decode_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "store_tokens_per_s": round(store["tokens_per_s"], 1),
+            "store_us": round(store["us"], 3)}
 
 
 def cpu_baseline(w, budget_s=10.0):
@@ -763,6 +786,8 @@ def main():
         result["prefill"] = time_prefill(dev)
         result["fresh_prefill"] = time_fresh_prefill(dev)
         del w
+        torch.cuda.empty_cache()
+        result["fp16"] = time_fp16(dev)
         torch.cuda.empty_cache()
         result["ragged"] = time_ragged(dev)
         result["long_context"] = [time_long_context(dev, b) for b in (1, 4)]
