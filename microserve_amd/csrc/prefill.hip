@@ -10,10 +10,10 @@
 //  * A workgroup covers 128 rows of one (sequence, kv head, block of query
 //    tokens).  A row is one (query token, q head) pair; the GQA group of the
 //    kv head fills the rows, so every K/V tile serves all the q heads that
-//    read it.  bf16 runs four waves of two 16-row blocks, so every K and V
-//    operand a wave reads from LDS feeds both, which halves LDS traffic per
-//    FLOP; fp16, whose query needs a third e4m3 part, runs eight waves of
-//    one block to stay within the register file.
+//    read it.  Four waves of two 16-row blocks, so every K operand a wave
+//    reads from LDS feeds both.  bf16 also shares each V^T operand between
+//    the blocks; fp16, whose query needs a third e4m3 part, computes one
+//    block's P and PV at a time to stay within the register file.
 //  * K/V tiles of 128 keys (one f8f6f4 MFMA contraction) are staged in LDS,
 //    double-buffered with one barrier per tile.  Rows are written with their
 //    16-byte chunks XOR-swizzled by (row / 2) % 8, which keeps the row
@@ -51,11 +51,11 @@
 namespace mskv {
 
 constexpr int kPStep = 128;  // keys per tile
-// A workgroup covers 128 rows.  bf16 (two query parts) runs 4 waves of two
-// 16-row blocks; fp16 (three parts) needs 24 more registers per block and
-// runs 8 waves of one block, which avoids spills.
+// A workgroup covers 128 rows: 4 waves of two 16-row blocks.  fp16's third
+// query part costs 16 registers, which it wins back by running the P and
+// PV work of its two blocks one after the other.
 template <int NQ> struct PShape {
-  static constexpr int blocks = NQ == 2 ? 2 : 1;  // 16-row blocks per wave
+  static constexpr int blocks = 2;  // 16-row blocks per wave
   static constexpr int waves = 8 / blocks;
   static constexpr int threads = 64 * waves;
 };
@@ -457,50 +457,100 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
       // drops it after: bf16 1.9% faster, fp16 unchanged.  Over the PV loop
       // alone it gained bf16 0.3-0.6% and cost fp16 6%.
       __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-      for (int tt = 0; tt < 8; ++tt) {
-        const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
-        const f32x4 rv = *reinterpret_cast<const f32x4*>(rvw + 16 * tt + 4 * g);
-#pragma unroll
-        for (int b = 0; b < kPBlocks; ++b) {
-          float y[4];
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-            y[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b])) * vsc[r];
-          const uint32_t h = pack_fp8x4(y[0], y[1], y[2], y[3]);
-          const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
-          const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
-          const uint32_t lo = pack_fp8x4(y[0] - h01[0], y[1] - h01[1], y[2] - h23[0],
-                                         y[3] - h23[1]);
-          const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
-          const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
-          lsum[b] = fmaf(h01[0] + l01[0], rv[0], lsum[b]);
-          lsum[b] = fmaf(h01[1] + l01[1], rv[1], lsum[b]);
-          lsum[b] = fmaf(h23[0] + l23[0], rv[2], lsum[b]);
-          lsum[b] = fmaf(h23[1] + l23[1], rv[3], lsum[b]);
-          p8h[b][tt] = (int)h;
-          p8l[b][tt] = (int)lo;
-        }
-      }
-#pragma unroll
-      for (int b = 0; b < kPBlocks; ++b) l[b] += __builtin_amdgcn_ldexpf(lsum[b], -kr[b]);
-      // O^T += V^T . P8^T, one 16-wide d tile per MFMA pair
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        i32x8 va;
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-              reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
-                  (__attribute__((address_space(3))) uint8_t*)vt + tr_row[qq] +
-                  ((16u * dt) ^ tr_swz[qq])));
-          va[2 * qq] = r[0];
-          va[2 * qq + 1] = r[1];
-        }
+      if constexpr (NQ == 3) {
+        // fp16: the third query part takes the registers of one block's P
+        // operands, so each block computes its P and runs its PV MFMAs in
+        // turn, reading V^T once per block
 #pragma unroll
         for (int b = 0; b < kPBlocks; ++b) {
-          acc[b][dt] = mfma_fp8_scale_b(va, p8h[b], acc[b][dt], 127 - kr[b]);
-          acc[b][dt] = mfma_fp8_scale_b(va, p8l[b], acc[b][dt], 127 - kr[b]);
+          i32x8 ph, pl;
+#pragma unroll
+          for (int tt = 0; tt < 8; ++tt) {
+            const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
+            const f32x4 rv = *reinterpret_cast<const f32x4*>(rvw + 16 * tt + 4 * g);
+            float y[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              y[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b])) * vsc[r];
+            const uint32_t h = pack_fp8x4(y[0], y[1], y[2], y[3]);
+            const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
+            const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
+            const uint32_t lo = pack_fp8x4(y[0] - h01[0], y[1] - h01[1], y[2] - h23[0],
+                                           y[3] - h23[1]);
+            const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
+            const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+            lsum[b] = fmaf(h01[0] + l01[0], rv[0], lsum[b]);
+            lsum[b] = fmaf(h01[1] + l01[1], rv[1], lsum[b]);
+            lsum[b] = fmaf(h23[0] + l23[0], rv[2], lsum[b]);
+            lsum[b] = fmaf(h23[1] + l23[1], rv[3], lsum[b]);
+            ph[tt] = (int)h;
+            pl[tt] = (int)lo;
+          }
+          l[b] += __builtin_amdgcn_ldexpf(lsum[b], -kr[b]);
+#pragma unroll
+          for (int dt = 0; dt < 8; ++dt) {
+            i32x8 va;
+#pragma unroll
+            for (int qq = 0; qq < 4; ++qq) {
+              const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                  reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
+                      (__attribute__((address_space(3))) uint8_t*)vt + tr_row[qq] +
+                      ((16u * dt) ^ tr_swz[qq])));
+              va[2 * qq] = r[0];
+              va[2 * qq + 1] = r[1];
+            }
+            acc[b][dt] = mfma_fp8_scale_b(va, ph, acc[b][dt], 127 - kr[b]);
+            acc[b][dt] = mfma_fp8_scale_b(va, pl, acc[b][dt], 127 - kr[b]);
+          }
+          // keep the next block's P work out of this block's PV
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+  #pragma unroll
+        for (int tt = 0; tt < 8; ++tt) {
+          const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
+          const f32x4 rv = *reinterpret_cast<const f32x4*>(rvw + 16 * tt + 4 * g);
+  #pragma unroll
+          for (int b = 0; b < kPBlocks; ++b) {
+            float y[4];
+  #pragma unroll
+            for (int r = 0; r < 4; ++r)
+              y[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b])) * vsc[r];
+            const uint32_t h = pack_fp8x4(y[0], y[1], y[2], y[3]);
+            const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
+            const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
+            const uint32_t lo = pack_fp8x4(y[0] - h01[0], y[1] - h01[1], y[2] - h23[0],
+                                           y[3] - h23[1]);
+            const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
+            const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
+            lsum[b] = fmaf(h01[0] + l01[0], rv[0], lsum[b]);
+            lsum[b] = fmaf(h01[1] + l01[1], rv[1], lsum[b]);
+            lsum[b] = fmaf(h23[0] + l23[0], rv[2], lsum[b]);
+            lsum[b] = fmaf(h23[1] + l23[1], rv[3], lsum[b]);
+            p8h[b][tt] = (int)h;
+            p8l[b][tt] = (int)lo;
+          }
+        }
+  #pragma unroll
+        for (int b = 0; b < kPBlocks; ++b) l[b] += __builtin_amdgcn_ldexpf(lsum[b], -kr[b]);
+        // O^T += V^T . P8^T, one 16-wide d tile per MFMA pair
+  #pragma unroll
+        for (int dt = 0; dt < 8; ++dt) {
+          i32x8 va;
+  #pragma unroll
+          for (int qq = 0; qq < 4; ++qq) {
+            const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+                reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
+                    (__attribute__((address_space(3))) uint8_t*)vt + tr_row[qq] +
+                    ((16u * dt) ^ tr_swz[qq])));
+            va[2 * qq] = r[0];
+            va[2 * qq + 1] = r[1];
+          }
+  #pragma unroll
+          for (int b = 0; b < kPBlocks; ++b) {
+            acc[b][dt] = mfma_fp8_scale_b(va, p8h[b], acc[b][dt], 127 - kr[b]);
+            acc[b][dt] = mfma_fp8_scale_b(va, p8l[b], acc[b][dt], 127 - kr[b]);
+          }
         }
       }
       __builtin_amdgcn_s_setprio(0);
