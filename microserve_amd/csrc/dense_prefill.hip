@@ -105,8 +105,13 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4, n = lane & 15;
-  const int s = blockIdx.z;
-  const int unit = blockIdx.y;
+  // grid (kv head units, sequences, query blocks): the query block varies
+  // slowest and runs last-first, so every sequence's longest blocks are
+  // dispatched before any shorter ones (longest-first across the whole
+  // grid, not within each sequence); measured 3.8% faster than query
+  // blocks varying fastest
+  const int s = blockIdx.y;
+  const int unit = blockIdx.x;
   const int kvh = unit / a.qgroups;
   const int qgi = unit - kvh * a.qgroups;
 
@@ -122,7 +127,7 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
   const int shift = lk - lq;  // query i sees keys j <= i + shift
   const int wave_tok = kDBlocks * a.tpr;
   const int wg_tok = kDWaves * wave_tok;
-  const int wg_q0 = (int)(gridDim.x - 1 - blockIdx.x) * wg_tok;
+  const int wg_q0 = (int)(gridDim.z - 1 - blockIdx.z) * wg_tok;
   if (wg_q0 >= lq) return;
   const int wg_qlast = min(lq, wg_q0 + wg_tok) - 1;
   const int kv_end = max(0, min(lk, wg_qlast + shift + 1));
@@ -360,8 +365,11 @@ extern "C" int mskv_prefill_attention(const void* query, const void* key, const 
   a.tpr = 16 / a.gc;
   a.scale_log2 = softmax_scale * mskv::kLog2e;
   const int per_wg = mskv::kDWaves * mskv::kDBlocks * a.tpr;
-  const dim3 grid((unsigned)((max_seqlen_q + per_wg - 1) / per_wg),
-                  (unsigned)(num_kv_heads * a.qgroups), (unsigned)num_seqs);
+  // grid y and z are limited to 65535
+  const int64_t qblocks = ((int64_t)max_seqlen_q + per_wg - 1) / per_wg;
+  if (num_seqs > 65535 || qblocks > 65535) return MSKV_EUNSUPPORTED;
+  const dim3 grid((unsigned)(num_kv_heads * a.qgroups), (unsigned)num_seqs,
+                  (unsigned)qblocks);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   if (act_dtype == MSKV_BFLOAT16)
     hipLaunchKernelGGL(mskv::dense_prefill_kernel<__bf16>, grid, dim3(mskv::kDThreads), 0, st, a);

@@ -143,8 +143,13 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int g = lane >> 4, n = lane & 15;
-  const int s = blockIdx.z;
-  const int unit = blockIdx.y;
+  // grid (kv head units, sequences, query blocks): the query block varies
+  // slowest and runs last-first, so every sequence's longest blocks are
+  // dispatched before any shorter ones (longest-first across the whole
+  // grid, not within each sequence): bf16 5.4%, fp16 3.9% faster than
+  // query blocks varying fastest
+  const int s = blockIdx.y;
+  const int unit = blockIdx.x;
   const int kvh = unit / a.qgroups;
   const int qgi = unit - kvh * a.qgroups;
 
@@ -158,7 +163,7 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
   const int prefix = lk - lq;
   const int wave_tok = kPBlocks * a.tpr;  // query tokens per wave
   const int wg_tok = kPWaves * wave_tok;
-  const int wg_q0 = (int)(gridDim.x - 1 - blockIdx.x) * wg_tok;
+  const int wg_q0 = (int)(gridDim.z - 1 - blockIdx.z) * wg_tok;
   if (wg_q0 >= lq || lq <= 0) return;
   const int wg_qlast = min(lq, wg_q0 + wg_tok) - 1;
   const int kv_end = min(min(lk, prefix + wg_qlast + 1), a.w * a.bs);
@@ -645,8 +650,11 @@ extern "C" int mskv_fp8_prefill_attention(
   a.w = max_blocks_per_seq;
   a.scale_log2 = softmax_scale * mskv::kLog2e;
   const int per_wg = 8 * a.tpr;  // 128 rows: 8 blocks of 16 rows
-  const dim3 grid((unsigned)((max_seqlen_q + per_wg - 1) / per_wg),
-                  (unsigned)(num_kv_heads * a.qgroups), (unsigned)num_seqs);
+  // grid y and z are limited to 65535
+  const int64_t qblocks = ((int64_t)max_seqlen_q + per_wg - 1) / per_wg;
+  if (num_seqs > 65535 || qblocks > 65535) return MSKV_EUNSUPPORTED;
+  const dim3 grid((unsigned)(num_kv_heads * a.qgroups), (unsigned)num_seqs,
+                  (unsigned)qblocks);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (act_dtype == MSKV_BFLOAT16)
     hipLaunchKernelGGL(mskv::prefill_fp8_kernel<__bf16>, grid,

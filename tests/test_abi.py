@@ -81,6 +81,10 @@ def test_argument_validation_without_launch():
     assert lib.mskv_fp8_prefill_attention(1, 1, 1, 1, 1, 1, 1, None, 0, 1, 2, 10, 5, 32, 8, 128, 256, 10, 4, 0.1, 1, None) == EINVAL
     # prefill: block size not a multiple of 128
     assert lib.mskv_fp8_prefill_attention(1, 1, 1, 1, 1, 1, None, None, 0, 1, 1, 10, 10, 32, 8, 128, 64, 10, 4, 0.1, 1, None) == EUNSUP
+    # prefill: more query blocks than a grid dimension holds (GQA 16: 8 tokens per block)
+    big_q = 8 * 65535 + 1
+    assert lib.mskv_fp8_prefill_attention(1, 1, 1, 1, 1, 1, None, None, 0, 1, 1, big_q, big_q, 128, 8, 128, 256, 10, 4, 0.1, 1, None) == EUNSUP
+    assert lib.mskv_prefill_attention(1, 1, 1, 1, 1, 1, 1, big_q, big_q, 4 * 65535 * 48 + 1, 32, 8, 128, 0.1, 1, None) == EUNSUP
 
 
 def test_new_entry_points_validate_without_launch():
