@@ -35,7 +35,8 @@
 //    the weights applied.
 //  * Online softmax in base 2 with a lazy rescale (slack 2^8; p <= 256 fits
 //    both fp16 and bf16); masks only on tiles that straddle the diagonal or
-//    the end of the keys; query blocks launch last-first.
+//    the end of the keys; query blocks launch last-first across the whole
+//    grid.
 #include <math.h>
 
 #include "mskv_device.h"
