@@ -41,8 +41,9 @@
 //    evaluated only on tiles that straddle the causal diagonal or the end
 //    of the keys; fully visible tiles skip them.
 //  * Query blocks are launched last-first across the whole grid, so the
-//    longest workgroups of every sequence start before any shorter one.  Pages are read through page-sized buffer resources; an
-//    invalid block id gives zero-length reads and its keys are masked.
+//    longest workgroups of every sequence start before any shorter one.
+//    Pages are read through page-sized buffer resources; an invalid block
+//    id gives zero-length reads and its keys are masked.
 #include <math.h>
 
 #include "mskv_device.h"
