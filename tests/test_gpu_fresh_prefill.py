@@ -35,6 +35,19 @@ def _check(q, k, v, cu_q, cu_k, lq, lk):
     return H.assert_attention_close(out, ref), out
 
 
+def test_fresh_prefill_empty_sequences_and_oversized_max_seqlen():
+    """Empty sequences at the start and in the middle of the batch, and
+    max_seqlen_q far above the longest sequence."""
+    lens = [0, 40, 0, 300]
+    q, k, v, cu_q, cu_k = _setup(409, lens, lens, 32, 8)
+    scale = H.D ** -0.5
+    out = varlen_attention(q.to(H.DEV), k.to(H.DEV), v.to(H.DEV), cu_q.to(H.DEV),
+                           cu_k.to(H.DEV), max(lens) + 1000, max(lens), scale)
+    torch.cuda.synchronize()
+    ref = O.dense_varlen_attention(q, k, v, cu_q, cu_k, scale)
+    H.assert_attention_close(out, ref)
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_fresh_prefill_ragged_batch(dtype):
     """Fresh sequences (Lq == Lk) of ragged lengths, including 1 and lengths

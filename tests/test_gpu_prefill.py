@@ -139,6 +139,22 @@ def test_varlen_prefill_dominant_keys_with_vanishing_values(v_mult):
     print(f"vanishing-V dominant keys (x{v_mult}): max_abs {max_abs:.4e} rel {rel:.4e}")
 
 
+def test_varlen_prefill_empty_sequences_and_oversized_max_seqlen():
+    """Sequences with no new tokens (one with a cached prefix, one empty) in
+    the batch, and max_seqlen_q far above the longest query: the extra
+    query blocks find nothing to do and every row matches the oracle."""
+    lq = [0, 50, 0, 130]
+    lk = [500, 50 + 300, 0, 130 + 77]
+    query, tables, caches, cu_q, cu_k = _varlen_setup(271, lq, lk, 32, 8)
+    scale = H.D ** -0.5
+    out = fp8_varlen_prefill_attention(query.to(H.DEV), *caches, tables.to(H.DEV),
+                                       cu_q.to(H.DEV), cu_k.to(H.DEV), max(lq) + 1000, scale)
+    torch.cuda.synchronize()
+    kc, vc, ks, vs = H.cache_to_numpy(*caches)
+    ref = O.varlen_prefill_attention(query, kc, vc, ks, vs, tables, cu_q, cu_k, scale)
+    H.assert_attention_close(out, ref)
+
+
 def test_chunk_prefill_single_equals_varlen():
     lq, lk = [100], [100 + 700]
     query, tables, caches, cu_q, cu_k = _varlen_setup(231, lq, lk, 32, 8)
