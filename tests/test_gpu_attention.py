@@ -137,3 +137,31 @@ def test_wrappers_reject_host_tensors_among_gpu_arguments():
     with pytest.raises(AssertionError, match="must be on"):
         qk_norm_rope_store(torch.zeros(3, dtype=torch.int64), q, key, key, None, None, 1e-6, tab,
                            tab, kc, vc, ks, vs, torch.zeros(3, dtype=torch.int64, device="cuda"))
+
+
+def test_empty_batches_are_no_ops():
+    """Zero tokens to store, a decode batch of zero sequences and prefill
+    calls with no query rows return empty results without launching."""
+    from microserve_amd import (fp8_chunk_prefill_attention, fp8_decode_attention,
+                                fp8_varlen_prefill_attention, store_fp8_kvcache,
+                                varlen_attention)
+    caches = H.alloc_cache(4)
+    before = [c.clone() for c in caches]
+    e = torch.zeros(0, 8, H.D, dtype=torch.bfloat16, device=H.DEV)
+    store_fp8_kvcache(e, e, *caches, torch.zeros(0, dtype=torch.int64, device=H.DEV))
+    q0 = torch.zeros(0, 32, H.D, dtype=torch.bfloat16, device=H.DEV)
+    out = fp8_decode_attention(q0, *caches, torch.zeros(0, dtype=torch.int32, device=H.DEV),
+                               torch.zeros(0, 2, dtype=torch.int32, device=H.DEV), 0.088)
+    assert out.shape == (0, 32, H.D)
+    table = torch.tensor([0, 1], dtype=torch.int32, device=H.DEV)
+    out = fp8_chunk_prefill_attention(q0, *caches, table, 100, 0.088)
+    assert out.shape == (0, 32, H.D)
+    cu0 = torch.zeros(2, dtype=torch.int32, device=H.DEV)
+    out = fp8_varlen_prefill_attention(q0, *caches, table.view(1, 2), cu0, cu0, 0, 0.088)
+    assert out.shape == (0, 32, H.D)
+    out = varlen_attention(q0, e, e, cu0, cu0, 0, 0, 0.088)
+    assert out.shape == (0, 32, H.D)
+    torch.cuda.synchronize()
+    for a, b in zip(caches, before):
+        assert torch.equal(a.view(torch.uint8) if a.dtype == torch.float8_e4m3fn else a,
+                           b.view(torch.uint8) if b.dtype == torch.float8_e4m3fn else b)
