@@ -159,7 +159,10 @@ def test_decode_block_relabel_and_split_invariance():
 
 def test_decode_ragged_fragmented():
     """Ragged lengths, log-uniform in [16, 32768], blocks sampled from a
-    fragmented pool, with the one-token append stored in the same step."""
+    fragmented pool, with the one-token append stored in the same step.
+    17 splits x 48 sequences is 816 eight-wave workgroups, over the launcher's
+    limit of 512, so this runs the 4-wave workgroup shape (the Qwen3-8B full
+    shape, 256 workgroups, runs the 8-wave one)."""
     gen = torch.Generator().manual_seed(101)
     b = 48
     lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(32768), generator=gen)).long().tolist()
