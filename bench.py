@@ -163,6 +163,100 @@ def cpu_baseline(w, budget_s=10.0):
                                 f"oracle, {store_s:.2f} s"}}
 
 
+C1_HQ, C1_BATCH, C1_POOL, C1_MAXLEN = 16, 4, 64, 1024
+
+
+def config1_workload(dev, seed=1):
+    """The reference's CPU-runnable case at the Qwen3-0.6B layer shape: 16 q
+    / 8 kv heads, head_dim 128, block 256, batch 4, context lengths uniform
+    in [1, 1024], block tables from a seeded permutation of a 64-block pool,
+    bf16 N(0,1) q/k/v.  One step stores every token of the batch with
+    store_fp8_kvcache, then runs one decode step
+    (tests/test_fp8_kv_attention.py:39-73 at this shape)."""
+    gen = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, C1_MAXLEN + 1, (C1_BATCH,), generator=gen)
+    pages = (lens + BS - 1) // BS
+    perm = torch.randperm(C1_POOL, generator=gen).to(torch.int32)
+    tables = torch.full((C1_BATCH, int(pages.max())), -1, dtype=torch.int32)
+    slots, at = [], 0
+    for b in range(C1_BATCH):
+        tables[b, :pages[b]] = perm[at:at + pages[b]]
+        at += int(pages[b])
+        pos = torch.arange(int(lens[b]))
+        slots.append(tables[b, pos // BS].long() * BS + pos % BS)
+    slots = torch.cat(slots)
+    n = slots.numel()
+    key = torch.randn(n, HK, D, generator=gen).bfloat16()
+    value = torch.randn(n, HK, D, generator=gen).bfloat16()
+    q = torch.randn(C1_BATCH, C1_HQ, D, generator=gen).bfloat16()
+    kc = torch.zeros(C1_POOL, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(C1_POOL, BS, HK, device=dev)
+    vs = torch.ones_like(ks)
+    return dict(lens=lens, tables=tables, slots=slots, key=key, value=value, q=q,
+                kc=kc, vc=vc, ks=ks, vs=vs, key_d=key.to(dev), value_d=value.to(dev),
+                slots_d=slots.to(dev), q_d=q.to(dev), tables_d=tables.to(dev),
+                seqlens_d=lens.to(torch.int32).to(dev))
+
+
+def config1_step(w, out=None):
+    from microserve_amd import fp8_decode_attention, store_fp8_kvcache
+    store_fp8_kvcache(w["key_d"], w["value_d"], w["kc"], w["vc"], w["ks"], w["vs"], w["slots_d"])
+    return fp8_decode_attention(w["q_d"], w["kc"], w["vc"], w["ks"], w["vs"], w["seqlens_d"],
+                                w["tables_d"], D ** -0.5, out=out)
+
+
+def time_config1(dev, iters=200, warmup=20, cpu_budget_s=8.0, cpu=True):
+    """The Qwen3-0.6B batch-4 store-then-decode step on the GPU (HIP events)
+    and, on the host cores in the same run, the oracle's store (numpy) and
+    decode (torch fp32) of the same step."""
+    import numpy as np
+    w = config1_workload(dev)
+    out = torch.empty_like(w["q_d"])
+    us = _time_steps(lambda i: config1_step(w, out), iters, warmup)
+    n = w["slots"].numel()
+    st_bytes = store_bytes(n, HK, D)
+    dec_bytes = decode_bytes_ragged(w["lens"], C1_HQ, HK, D)
+    res = {"workload": "Qwen3-0.6B layer, 16 q / 8 kv heads, batch 4, context U[1, 1024] "
+                       f"(lengths {w['lens'].tolist()}), 64-block permuted pool: store of "
+                       f"every token ({n}) then one decode step",
+           "us": round(us, 2), "tokens_stored": n, "bytes": st_bytes + dec_bytes,
+           "gbs": round((st_bytes + dec_bytes) / us / 1e3, 1),
+           "store_tokens_per_s": round(n / us * 1e6, 1),
+           "note": "a 32 MB pool: the step runs from the caches and is launch-latency bound, "
+                   "so GB/s here is not an HBM figure"}
+    if not cpu:
+        return res
+    from oracle import fp8_oracle as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    kc = np.zeros((C1_POOL, BS, HK, D), np.uint8)
+    vc = np.zeros_like(kc)
+    ks = np.ones((C1_POOL, BS, HK), np.float32)
+    vs = np.ones_like(ks)
+    kf, vf, sl = w["key"].float().numpy(), w["value"].float().numpy(), w["slots"].numpy()
+    t_store = t_dec = 0.0
+    reps = 0
+    while t_store + t_dec < cpu_budget_s:
+        t0 = time.perf_counter()
+        O.store_fp8_kvcache(kf, vf, kc, vc, ks, vs, sl)
+        t1 = time.perf_counter()
+        O.decode_attention(w["q"], kc, vc, ks, vs, w["lens"], w["tables"], D ** -0.5)
+        t2 = time.perf_counter()
+        t_store += t1 - t0
+        t_dec += t2 - t1
+        reps += 1
+    res["cpu_baseline"] = {
+        "store_tokens_per_s": round(reps * n / t_store, 1),
+        "store_cores": 1,
+        "decode_gbs": round(reps * dec_bytes / t_dec / 1e9, 3),
+        "decode_cores": torch.get_num_threads(),
+        "step_us": round((t_store + t_dec) / reps * 1e6, 1),
+        "kind": "port",
+        "sample": f"{reps} repetitions of the whole step: numpy store oracle (one core), "
+                  f"torch fp32 decode oracle, {t_store + t_dec:.1f} s"}
+    return res
+
+
 PRE_SEQS, PRE_CACHED, PRE_NEW = 8, 8192, 2048
 FP8_PEAK_TFLOPS = 5000.0
 
@@ -174,12 +268,12 @@ def prefill_flops(seqs, cached, new, hq, d):
     return 4 * d * visits * hq * seqs
 
 
-def time_prefill(dev, iters=20, warmup=3, dtype=torch.bfloat16):
+def prefill_workload(dev, dtype=torch.bfloat16):
     """Varlen chunked prefill: 8 sequences x (8192 cached + 2048 new tokens),
     32 q / 8 kv heads, q/k/v N(0,1) (bf16 by default) with 1% of K entries
     x20, all 10240 tokens of each sequence stored first (as Attention
-    does)."""
-    from microserve_amd import fp8_varlen_prefill_attention, store_fp8_kvcache
+    does).  Returns the tensors one prefill call reads."""
+    from microserve_amd import store_fp8_kvcache
     gen = torch.Generator().manual_seed(77)
     lk = PRE_CACHED + PRE_NEW
     pages = lk // BS
@@ -199,21 +293,29 @@ def time_prefill(dev, iters=20, warmup=3, dtype=torch.bfloat16):
     q = torch.randn(PRE_SEQS * PRE_NEW, HQ, D, generator=gen).to(dtype).to(dev)
     cu_q = torch.arange(0, PRE_SEQS + 1, dtype=torch.int32, device=dev) * PRE_NEW
     cu_k = torch.arange(0, PRE_SEQS + 1, dtype=torch.int32, device=dev) * lk
-    tables = tables.to(dev)
+    return dict(q=q, kc=kc, vc=vc, ks=ks, vs=vs, tables=tables.to(dev), cu_q=cu_q, cu_k=cu_k,
+                max_seqlen_q=PRE_NEW)
 
-    def run():
-        return fp8_varlen_prefill_attention(q, kc, vc, ks, vs, tables, cu_q, cu_k,
-                                            PRE_NEW, D ** -0.5)
 
+def run_prefill(w):
+    from microserve_amd import fp8_varlen_prefill_attention
+    return fp8_varlen_prefill_attention(w["q"], w["kc"], w["vc"], w["ks"], w["vs"], w["tables"],
+                                        w["cu_q"], w["cu_k"], w["max_seqlen_q"], D ** -0.5)
+
+
+def time_prefill(dev, iters=20, warmup=3, dtype=torch.bfloat16):
+    """The varlen chunked prefill workload (prefill_workload), HIP-event time
+    per call."""
+    w = prefill_workload(dev, dtype)
     for _ in range(warmup):
-        run()
+        run_prefill(w)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(iters)]
     for e0, e1 in evs:
         e0.record(stream)
-        run()
+        run_prefill(w)
         e1.record(stream)
     torch.cuda.synchronize()
     us = sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
@@ -255,12 +357,13 @@ def _fill_pages(dev, kc, vc, ks, vs, pages, gen, chunk_pages=512):
         store_fp8_kvcache(key, value, kc, vc, ks, vs, slots)
 
 
-def time_ragged(dev, iters=50, warmup=5):
+def ragged_workload(dev):
     """Ragged decode stress at the Qwen3-8B shape: batch 256, context lengths
     log-uniform in [16, 32768], each sequence's blocks sampled without
-    replacement from a 40,000-block pool; one step is the one-token
-    store_kvcache append of every sequence followed by the decode."""
-    from microserve_amd import fp8_decode_attention, store_fp8_kvcache
+    replacement from a 40,000-block pool, every page filled by
+    store_fp8_kvcache from bf16 N(0,1); one step is the one-token
+    store_kvcache append of every sequence (at its last position) followed
+    by the decode.  Returns the step's tensors."""
     gen = torch.Generator().manual_seed(3)
     b, pool = 256, 40000
     lens = torch.exp(torch.empty(b).uniform_(float(torch.log(torch.tensor(16.0))),
@@ -279,27 +382,51 @@ def time_ragged(dev, iters=50, warmup=5):
     ks = torch.ones(pool, BS, HK, device=dev)
     vs = torch.ones_like(ks)
     _fill_pages(dev, kc, vc, ks, vs, perm[:at], gen)
-    tables_d = tables.to(dev)
-    seqlens = lens.to(torch.int32).to(dev)
     # the appended token of each sequence is its last position
     last = (lens - 1)
-    slots = (tables[torch.arange(b), last // BS].long() * BS + last % BS).to(dev)
-    knew = torch.randn(b, HK, D, generator=gen).bfloat16().to(dev)
-    vnew = torch.randn(b, HK, D, generator=gen).bfloat16().to(dev)
-    q = torch.randn(b, HQ, D, generator=gen).bfloat16().to(dev)
-    out = torch.empty_like(q)
+    slots = (tables[torch.arange(b), last // BS].long() * BS + last % BS)
+    knew = torch.randn(b, HK, D, generator=gen).bfloat16()
+    vnew = torch.randn(b, HK, D, generator=gen).bfloat16()
+    q = torch.randn(b, HQ, D, generator=gen).bfloat16()
+    return dict(lens=lens, tables=tables, tables_d=tables.to(dev),
+                seqlens=lens.to(torch.int32).to(dev), kc=kc, vc=vc, ks=ks, vs=vs,
+                slots=slots, slots_d=slots.to(dev), knew=knew, knew_d=knew.to(dev),
+                vnew=vnew, vnew_d=vnew.to(dev), q=q, q_d=q.to(dev))
+
+
+def ragged_append(w):
+    from microserve_amd import store_fp8_kvcache
+    store_fp8_kvcache(w["knew_d"], w["vnew_d"], w["kc"], w["vc"], w["ks"], w["vs"], w["slots_d"])
+
+
+def ragged_decode(w, out=None):
+    from microserve_amd import fp8_decode_attention
+    return fp8_decode_attention(w["q_d"], w["kc"], w["vc"], w["ks"], w["vs"], w["seqlens"],
+                                w["tables_d"], D ** -0.5, out=out)
+
+
+def time_ragged(dev, iters=50, warmup=5):
+    """The ragged step (ragged_workload): append + decode, and the append's
+    store alone (256 tokens, a launch-latency-bound call)."""
+    w = ragged_workload(dev)
+    b = w["lens"].numel()
+    out = torch.empty_like(w["q_d"])
 
     def step(i):
-        store_fp8_kvcache(knew, vnew, kc, vc, ks, vs, slots)
-        fp8_decode_attention(q, kc, vc, ks, vs, seqlens, tables_d, D ** -0.5, out=out)
+        ragged_append(w)
+        ragged_decode(w, out)
 
     us = _time_steps(step, iters, warmup)
+    append_us = _time_steps(lambda i: ragged_append(w), iters, warmup)
+    lens = w["lens"]
     nbytes = decode_bytes_ragged(lens, HQ, HK, D) + store_bytes(b, HK, D)
     return {"workload": "ragged decode, batch 256, context log-uniform [16, 32768], "
                         "40k-block fragmented pool, with the one-token append store",
             "tokens": int(lens.sum()), "us": round(us, 2), "bytes": nbytes,
             "gbs": round(nbytes / us / 1e3, 1),
-            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)}
+            "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4),
+            "append_us": round(append_us, 2),
+            "append_tokens_per_s": round(b / append_us * 1e6, 1)}
 
 
 def decode_bytes_ragged(lens, hq, hk, d, act_bytes=2):
@@ -684,6 +811,8 @@ def main():
                     help="time only the ragged and long-context decode workloads")
     ap.add_argument("--norm-rope-only", action="store_true",
                     help="time only the fused q/k norm + rotary + store prologue")
+    ap.add_argument("--config1-only", action="store_true",
+                    help="time only the Qwen3-0.6B batch-4 store + decode step")
     ap.add_argument("--step-inputs-only", action="store_true",
                     help="time only the per-step input builder")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -699,13 +828,16 @@ def main():
         return
     if args.shapes_only:
         print(json.dumps({"ragged": time_ragged(dev),
-                          "long_context": [time_long_context(dev, b) for b in (1, 4)]}))
+                          "long_context": [time_long_context(dev, b) for b in (1, 2, 4)]}))
         return
     if args.fresh_only:
         print(json.dumps({"fresh_prefill": time_fresh_prefill(dev)}))
         return
     if args.norm_rope_only:
         print(json.dumps({"qk_norm_rope_store": time_norm_rope(dev)}))
+        return
+    if args.config1_only:
+        print(json.dumps({"config1": time_config1(dev, cpu=not args.no_cpu)}))
         return
     if args.step_inputs_only:
         print(json.dumps({"step_inputs": time_step_inputs(dev)}))
@@ -783,14 +915,18 @@ def main():
     if not args.no_cpu and not args.decode_only:
         result["cpu_baseline"] = cpu_baseline(w)
     if not args.decode_only:
+        result["config1"] = time_config1(dev, cpu=not args.no_cpu)
         result["prefill"] = time_prefill(dev)
+        # fp16 activations, the type the reference requires with an FP8
+        # cache (Config.py:35-36)
+        result["prefill_fp16"] = time_prefill(dev, dtype=torch.float16)
         result["fresh_prefill"] = time_fresh_prefill(dev)
         del w
         torch.cuda.empty_cache()
         result["fp16"] = time_fp16(dev)
         torch.cuda.empty_cache()
         result["ragged"] = time_ragged(dev)
-        result["long_context"] = [time_long_context(dev, b) for b in (1, 4)]
+        result["long_context"] = [time_long_context(dev, b) for b in (1, 2, 4)]
         result["step_inputs"] = time_step_inputs(dev)
         result["qk_norm_rope_store"] = time_norm_rope(dev)
     print(json.dumps(result), flush=True)

@@ -265,7 +265,7 @@ def decode_attention_loop(query, k_cache, v_cache, k_scale_cache,
 
 def varlen_prefill_attention(query, k_cache, v_cache, k_scale_cache,
                              v_scale_cache, block_tables, cu_seqlens_q,
-                             cu_seqlens_k, softmax_scale) -> torch.Tensor:
+                             cu_seqlens_k, softmax_scale, rows=None) -> torch.Tensor:
     """Causal paged prefill over a varlen batch, float32.
 
     Sequence ``s`` owns query rows ``cu_q[s]..cu_q[s+1]`` and a context of
@@ -273,7 +273,9 @@ def varlen_prefill_attention(query, k_cache, v_cache, k_scale_cache,
     ones (they are stored before attention, ``attention.py:41-43,56-60``).
     Query ``i`` sees positions ``< prefix + i + 1`` with
     ``prefix = Lk - Lq`` (``fp8_chunk_prefill_attention.py:52-54``).
-    Returns float32 ``[total_q, H_q, D]``.
+    Returns float32 ``[total_q, H_q, D]``; with ``rows`` (ascending query
+    row indices into ``total_q``), only those rows, ``[len(rows), H_q, D]``,
+    each computed exactly as in the full result.
     """
     q = _as_t(query).float()
     tq, hq, d = q.shape
@@ -282,22 +284,31 @@ def varlen_prefill_attention(query, k_cache, v_cache, k_scale_cache,
     cu_q = [int(x) for x in _as_t(cu_seqlens_q).reshape(-1).tolist()]
     cu_k = [int(x) for x in _as_t(cu_seqlens_k).reshape(-1).tolist()]
     tables = _as_t(block_tables, torch.int64)
-    out = torch.zeros(tq, hq, d, dtype=torch.float32)
+    if rows is None:
+        sel_all = torch.arange(tq)
+    else:
+        sel_all = _as_t(rows, torch.int64).reshape(-1)
+        assert bool((sel_all[1:] > sel_all[:-1]).all()), "rows must be ascending"
+    out = torch.zeros(sel_all.numel(), hq, d, dtype=torch.float32)
     for s in range(len(cu_q) - 1):
         lq = cu_q[s + 1] - cu_q[s]
         lk = cu_k[s + 1] - cu_k[s]
         if lq <= 0:
             continue
+        at = ((sel_all >= cu_q[s]) & (sel_all < cu_q[s + 1])).nonzero().view(-1)
+        if at.numel() == 0:
+            continue
+        i = sel_all[at] - cu_q[s]                                    # query index in the sequence
         prefix = lk - lq
         k = dequant_gather(k_cache, k_scale_cache, tables[s], lk)   # [Lk, H_kv, D]
         v = dequant_gather(v_cache, v_scale_cache, tables[s], lk)
-        qs = q[cu_q[s]:cu_q[s + 1]].view(lq, hk, group, d)
+        qs = q[cu_q[s] + i].view(i.numel(), hk, group, d)
         scores = torch.einsum("ikgd,lkd->kgil", qs, k) * softmax_scale
         pos = torch.arange(lk)[None, :]
-        visible = (prefix + torch.arange(lq) + 1)[:, None]
+        visible = (prefix + i + 1)[:, None]
         scores = scores.masked_fill(~(pos < visible)[None, None], float("-inf"))
         o = torch.einsum("kgil,lkd->ikgd", scores.softmax(-1), v)
-        out[cu_q[s]:cu_q[s + 1]] = o.reshape(lq, hq, d)
+        out[at] = o.reshape(i.numel(), hq, d)
     return out
 
 

@@ -75,3 +75,38 @@ def oracle_store_numpy(key, value, slots, num_blocks, block_size=BLOCK, kv_heads
     O.store_fp8_kvcache(key.float().numpy(), value.float().numpy(), kc, vc, ks, vs,
                         slots.numpy())
     return kc, vc, ks, vs
+
+
+def oracle_quantize_threaded(x: torch.Tensor, chunk: int = 4096):
+    """The oracle's ``quantize_rows`` over a large [N, H, D] tensor (any
+    device), in chunks on a thread pool (numpy's array operations release
+    the GIL).  Returns (uint8 bytes [N, H, D], float32 scales [N, H])."""
+    import os
+    from concurrent.futures import ThreadPoolExecutor
+    n = x.shape[0]
+    q = np.empty(tuple(x.shape), np.uint8)
+    s = np.empty(tuple(x.shape[:-1]), np.float32)
+
+    def work(i):
+        qi, si = O.quantize_rows(x[i:i + chunk].float().cpu().numpy())
+        q[i:i + chunk] = qi
+        s[i:i + chunk] = si
+
+    with ThreadPoolExecutor(min(16, os.cpu_count() or 1)) as ex:
+        list(ex.map(work, range(0, n, chunk)))
+    return q, s
+
+
+def compact_cache(caches, tables):
+    """The blocks ``tables`` uses, copied to the host as uint8 / float32 numpy
+    arrays, and the tables renumbered to them (a block relabelling, which
+    leaves every attention output unchanged)."""
+    t = tables.cpu().long()
+    used = t[t >= 0].unique()
+    remap = torch.full((int(used.max()) + 1 if used.numel() else 1,), -1, dtype=torch.long)
+    remap[used] = torch.arange(used.numel())
+    new = torch.where(t >= 0, remap[t.clamp_min(0)], torch.full_like(t, -1)).to(torch.int32)
+    idx = used.to(caches[0].device)
+    kc, vc, ks, vs = caches
+    return (kc.view(torch.uint8)[idx].cpu().numpy(), vc.view(torch.uint8)[idx].cpu().numpy(),
+            ks[idx].cpu().numpy(), vs[idx].cpu().numpy()), new

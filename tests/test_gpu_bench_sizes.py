@@ -1,0 +1,120 @@
+"""GPU parity at the sizes bench.py reports, on the very tensors it times
+(its workload builders are imported, not restated):
+
+* the Qwen3-8B pool fill (2 x 262,144 tokens): every cache byte and scale
+  against the oracle's quantizer and the placement rule
+  (``fp8_kv_cache.py:24-39``), and both decode table sets against the
+  oracle's decode;
+* the ragged batch-256 step over the 40,000-block pool: the one-token
+  append's bytes, then every output row of the decode that follows it
+  (``fp8_decode_attention.py:16-58``);
+* the 8 x (8192 cached + 2048 new) chunked prefill with 1% x20 K outliers,
+  bf16 and fp16: every output finite, and 512 query tokens per sequence (the
+  first and last token of every 128-row workgroup block, the sequence's last
+  token, the rest random) against the oracle over ``prefix + i + 1`` keys
+  (``fp8_chunk_prefill_attention.py:52-54``).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from oracle import fp8_oracle as O
+from tests import gpu_helpers as H
+
+pytestmark = pytest.mark.gpu
+
+
+def test_store_fill_qwen3_8b_every_byte_and_decode():
+    w = bench.build_workload(H.DEV)
+    torch.cuda.synchronize()
+    kc8 = w["kc"].view(torch.uint8).view(-1, bench.HK, bench.D)
+    vc8 = w["vc"].view(torch.uint8).view(-1, bench.HK, bench.D)
+    ksf = w["ks"].view(-1, bench.HK)
+    vsf = w["vs"].view(-1, bench.HK)
+    written = torch.zeros(kc8.shape[0], dtype=torch.bool)
+    for half, (key, value, slots) in enumerate(w["fills"]):
+        n = slots.numel()
+        assert n == 262144
+        print(f"fill half {half}: {n} tokens", flush=True)
+        kq, kscale = H.oracle_quantize_threaded(key)
+        vq, vscale = H.oracle_quantize_threaded(value)
+        # row slot of the flattened cache holds token t (fp8_kv_cache.py:29-39)
+        assert np.array_equal(kc8[slots].cpu().numpy(), kq), "k bytes"
+        assert np.array_equal(vc8[slots].cpu().numpy(), vq), "v bytes"
+        assert np.array_equal(ksf[slots].cpu().numpy().view(np.uint32), kscale.view(np.uint32))
+        assert np.array_equal(vsf[slots].cpu().numpy().view(np.uint32), vscale.view(np.uint32))
+        written[slots.cpu()] = True
+    assert bool(written.all())  # the two halves tile the whole 2048-block pool
+    scale = bench.D ** -0.5
+    from microserve_amd import fp8_decode_attention
+    for half in range(2):
+        out = fp8_decode_attention(w["query"], w["kc"], w["vc"], w["ks"], w["vs"], w["seqlens"],
+                                   w["tables"][half], scale)
+        torch.cuda.synchronize()
+        caches, tables = H.compact_cache((w["kc"], w["vc"], w["ks"], w["vs"]), w["tables"][half])
+        ref = O.decode_attention(w["query"].cpu(), *caches, w["seqlens"].cpu(), tables, scale)
+        max_abs, rel = H.assert_attention_close(out, ref)
+        print(f"decode half {half}: max_abs {max_abs:.3e} rel {rel:.3e}", flush=True)
+
+
+def test_ragged_batch256_step_append_and_decode():
+    w = bench.ragged_workload(H.DEV)
+    lens = w["lens"]
+    print(f"ragged: {lens.numel()} sequences, {int(lens.sum())} tokens, "
+          f"table width {w['tables'].shape[1]}", flush=True)
+    bench.ragged_append(w)
+    out = bench.ragged_decode(w)
+    torch.cuda.synchronize()
+    # the appended rows: bit-exact at their slots
+    kq, kscale = O.quantize_rows(w["knew"].float().numpy())
+    vq, vscale = O.quantize_rows(w["vnew"].float().numpy())
+    rows = w["slots_d"]
+    assert np.array_equal(w["kc"].view(torch.uint8).view(-1, 8, 128)[rows].cpu().numpy(), kq)
+    assert np.array_equal(w["vc"].view(torch.uint8).view(-1, 8, 128)[rows].cpu().numpy(), vq)
+    assert np.array_equal(w["ks"].view(-1, 8)[rows].cpu().numpy().view(np.uint32),
+                          kscale.view(np.uint32))
+    assert np.array_equal(w["vs"].view(-1, 8)[rows].cpu().numpy().view(np.uint32),
+                          vscale.view(np.uint32))
+    # every output row against the oracle's decode over the same cache
+    caches, tables = H.compact_cache((w["kc"], w["vc"], w["ks"], w["vs"]), w["tables"])
+    ref = O.decode_attention(w["q"], *caches, lens, tables, bench.D ** -0.5)
+    max_abs, rel = H.assert_attention_close(out, ref)
+    print(f"ragged decode: max_abs {max_abs:.3e} rel {rel:.3e}", flush=True)
+
+
+def _sampled_rows(gen, seqs, lq, per_seq=512, block_tokens=32):
+    rows = []
+    for s in range(seqs):
+        pick = set()
+        for j in range(0, lq, block_tokens):
+            pick.update((j, min(lq, j + block_tokens) - 1))
+        pick.add(lq - 1)
+        rest = torch.randperm(lq, generator=gen).tolist()
+        for i in rest:
+            if len(pick) >= per_seq:
+                break
+            pick.add(i)
+        rows.extend(s * lq + i for i in sorted(pick))
+    return torch.tensor(rows)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_chunked_prefill_full_size_sampled_rows(dtype):
+    w = bench.prefill_workload(H.DEV, dtype)
+    out = bench.run_prefill(w)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "non-finite output"
+    rows = _sampled_rows(torch.Generator().manual_seed(5), bench.PRE_SEQS, bench.PRE_NEW)
+    assert rows.numel() == bench.PRE_SEQS * 512
+    # 128 rows of a workgroup block are 32 query tokens at GQA 4
+    assert bench.HQ // bench.HK == 4
+    kc = w["kc"].view(torch.uint8).cpu().numpy()
+    vc = w["vc"].view(torch.uint8).cpu().numpy()
+    ref = O.varlen_prefill_attention(w["q"].cpu(), kc, vc, w["ks"].cpu().numpy(),
+                                     w["vs"].cpu().numpy(), w["tables"].cpu(), w["cu_q"].cpu(),
+                                     w["cu_k"].cpu(), bench.D ** -0.5, rows=rows)
+    max_abs, rel = H.assert_attention_close(out[rows.to(H.DEV)], ref)
+    print(f"prefill {dtype}: {rows.numel()} rows, max_abs {max_abs:.3e} rel {rel:.3e}",
+          flush=True)

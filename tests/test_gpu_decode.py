@@ -157,17 +157,32 @@ def test_decode_block_relabel_and_split_invariance():
     assert (solo.float() - out[:1].float()).abs().max().item() < 1e-2
 
 
-def test_decode_ragged_fragmented():
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_ragged_fragmented(dtype):
     """Ragged lengths, log-uniform in [16, 32768], blocks sampled from a
-    fragmented pool, with the one-token append stored in the same step.
-    17 splits x 48 sequences is 816 eight-wave workgroups, over the launcher's
-    limit of 512, so this runs the 4-wave workgroup shape (the Qwen3-8B full
-    shape, 256 workgroups, runs the 8-wave one)."""
+    fragmented pool.  17 splits x 48 sequences is 816 eight-wave workgroups,
+    over the launcher's limit for that shape, so this runs the 4-wave
+    workgroup shape (the Qwen3-8B full shape, 256 workgroups, runs the
+    8-wave one), in both activation types."""
     gen = torch.Generator().manual_seed(101)
     b = 48
     lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(32768), generator=gen)).long().tolist()
     pages = sum((n + 255) // 256 for n in lens)
-    query, tables, caches = _setup(102, lens, 32, 8, pages + 97)
+    query, tables, caches = _setup(102, lens, 32, 8, pages + 97, dtype)
+    _run_and_check(query, lens, tables, caches)
+
+
+def test_decode_narrow_workgroups_wide_gqa_group():
+    """GQA 32 (64 q / 2 kv heads: two 16-head units per kv head) on the
+    4-wave workgroup shape: 96 sequences x 16 splits of one 8-wave
+    workgroup each is over the launcher's limit."""
+    gen = torch.Generator().manual_seed(105)
+    b = 96
+    lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(16384), generator=gen)).long().tolist()
+    lens[0] = 16384                      # the table is 64 pages wide
+    assert decode_num_splits(b, 64, 2, 64, H.BLOCK) == 16
+    pages = sum((n + 255) // 256 for n in lens)
+    query, tables, caches = _setup(106, lens, 64, 2, pages + 5, torch.float16)
     _run_and_check(query, lens, tables, caches)
 
 

@@ -270,6 +270,32 @@ def test_varlen_prefill_vs_loop_and_sdpa():
     assert np.abs(a[0] - dec[0].numpy()).max() < 1e-5
 
 
+def test_varlen_prefill_selected_rows():
+    """``rows=`` computes only the listed query rows: they equal the same rows
+    of the full result and the float64 loop, in every sequence, and a row
+    moved by one position (a wrong causal bound for the subset) does not."""
+    rng = np.random.default_rng(61)
+    bs, hq, hk, d = 16, 4, 2, 32
+    lk = [30, 12, 40]
+    lq = [9, 12, 0]
+    tables = np.array([[4, 1, -1], [0, -1, -1], [2, 3, 5]], np.int32)
+    kc, vc, ks, vs = _filled_cache(rng, 6, bs, hk, d, tables, lk)
+    cu_q = np.array([0, 9, 21, 21], np.int32)
+    cu_k = np.array([0, 30, 42, 82], np.int32)
+    q = rng.standard_normal((21, hq, d)).astype(np.float32)
+    sc = d ** -0.5
+    full = O.varlen_prefill_attention(q, kc, vc, ks, vs, tables, cu_q, cu_k, sc)
+    rows = np.array([0, 3, 8, 9, 15, 20])
+    sub = O.varlen_prefill_attention(q, kc, vc, ks, vs, tables, cu_q, cu_k, sc, rows=rows)
+    assert sub.shape == (6, hq, d)
+    assert torch.allclose(sub, full[rows], atol=1e-6)
+    loop = O.varlen_prefill_attention_loop(torch.from_numpy(q), kc, vc, ks, vs, tables, cu_q,
+                                           cu_k, sc)
+    assert np.abs(sub.numpy() - loop[rows]).max() < 1e-5
+    # every row differs from its neighbour's result (the check can fail)
+    assert (sub[1:] - full[rows[1:] - 1]).abs().max(-1).values.min() > 1e-4
+
+
 def test_dense_varlen_vs_loop_sdpa_and_paged_oracle():
     """The fresh-PREFILL oracle: float64 loop, SDPA on the square causal
     case, and the paged oracle on a cache holding the same K/V exactly."""
