@@ -108,6 +108,38 @@ int mskv_fp8_decode_attention(const void* query, const void* k_cache,
                               int act_dtype, int num_splits, void* workspace,
                               size_t workspace_bytes, void* stream);
 
+/* Split-partials scratch the allocation-free decode holds per GPU. */
+#define MSKV_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+
+/*
+ * mskv_fp8_decode_attention without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving
+ * loops and harnesses that forbid hipMalloc).  It has no counterpart in the
+ * reference.  The split partials go to a library-owned device array of
+ * MSKV_DECODE_NOALLOC_SCRATCH_BYTES (32 MiB) on each GPU, held until the
+ * process ends; shapes whose mskv_decode_workspace_bytes exceeds it are
+ * rejected with MSKV_EWORKSPACE (e.g. batch 64 x 4096 tokens at 32 q heads
+ * needs 4.2 MB, batch 4 x 131072 at 64 q heads 16.9 MB).  The call makes no
+ * hipMalloc/hipFree; the array's address on the current device is looked
+ * up once, on that device's first call.  No part of the array needs to
+ * start at zero.  Every call on one GPU shares that GPU's array: calls that
+ * may overlap on one GPU (different streams, or one graph replayed while
+ * another call runs) race on it and must be serialized by the caller.
+ * Arguments and results are mskv_fp8_decode_attention's.
+ */
+int mskv_fp8_decode_attention_noalloc(const void* query, const void* k_cache,
+                                      const void* v_cache,
+                                      const float* k_scale_cache,
+                                      const float* v_scale_cache,
+                                      const int32_t* cache_seqlens,
+                                      const int32_t* block_tables, void* out,
+                                      int batch, int num_q_heads,
+                                      int num_kv_heads, int head_dim,
+                                      int block_size, int64_t num_blocks,
+                                      int max_blocks_per_seq,
+                                      float softmax_scale, int act_dtype,
+                                      int num_splits, void* stream);
+
 /*
  * Causal paged prefill over the FP8 cache for a varlen batch whose new
  * tokens are already stored in the cache.

@@ -35,6 +35,10 @@ _PROTOS = {
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
         _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_f32,
         _c_int, _c_int, _vp, _c_size, _vp]),
+    "mskv_fp8_decode_attention_noalloc": (_c_int, [
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+        _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_f32,
+        _c_int, _c_int, _vp]),
     "mskv_fp8_prefill_attention": (_c_int, [
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _vp,
         _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_int, _c_i64,

@@ -47,6 +47,8 @@
 //    tokens are masked, so a bad table entry cannot fault.
 #include <math.h>
 
+#include <mutex>
+
 #include "mskv_device.h"
 #include "../../include/mskv.h"
 
@@ -62,6 +64,8 @@ constexpr int kTargetWaves = 2048;
 constexpr int kWavesPerWG = 8;
 constexpr int kNarrowWaves = 4;       // workgroup shape for grids of many rounds
 constexpr int64_t kWideGridMax = 512; // 8-wave workgroups: two per CU of 256
+// Largest split-partials scratch the allocation-free entry point serves
+constexpr size_t kNoAllocScratchBytes = MSKV_DECODE_NOALLOC_SCRATCH_BYTES;
 
 // Orders this wave's LDS writes before its later LDS reads (LDS executes one
 // wave's instructions in issue order, so no workgroup barrier is needed).
@@ -554,22 +558,25 @@ extern "C" size_t mskv_decode_workspace_bytes(int batch, int num_q_heads,
   return (size_t)batch * num_q_heads * num_splits * (head_dim + 1) * sizeof(float);
 }
 
-extern "C" int mskv_fp8_decode_attention(
-    const void* query, const void* k_cache, const void* v_cache,
-    const float* k_scale_cache, const float* v_scale_cache,
-    const int32_t* cache_seqlens, const int32_t* block_tables, void* out,
-    int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
-    int64_t num_blocks, int max_blocks_per_seq, float softmax_scale,
-    int act_dtype, int num_splits, void* workspace, size_t workspace_bytes,
-    void* stream) {
+namespace mskv {
+
+// Validates a decode call and launches it with `workspace` as the split
+// partials ([batch, hq, splits, 128] outputs, then [batch, hq, splits]
+// lse values); `workspace_bytes` is what the caller's buffer holds.
+static int decode_checked(const void* query, const void* k_cache, const void* v_cache,
+                          const float* k_scale_cache, const float* v_scale_cache,
+                          const int32_t* cache_seqlens, const int32_t* block_tables, void* out,
+                          int batch, int num_q_heads, int num_kv_heads, int head_dim,
+                          int block_size, int64_t num_blocks, int max_blocks_per_seq,
+                          float softmax_scale, int act_dtype, int num_splits, void* workspace,
+                          size_t workspace_bytes, void* stream) {
   if (batch < 0 || num_q_heads <= 0 || num_kv_heads <= 0 || block_size <= 0 ||
       num_blocks < 0 || max_blocks_per_seq <= 0 || num_splits <= 0)
     return MSKV_EINVAL;
   if (act_dtype != MSKV_FLOAT16 && act_dtype != MSKV_BFLOAT16) return MSKV_EINVAL;
   if (num_q_heads % num_kv_heads != 0) return MSKV_EINVAL;
   const int group = num_q_heads / num_kv_heads;
-  if (head_dim != mskv::kHeadDim || block_size % mskv::kStep != 0 ||
-      (group > 16 && group % 16 != 0))
+  if (head_dim != kHeadDim || block_size % kStep != 0 || (group > 16 && group % 16 != 0))
     return MSKV_EUNSUPPORTED;
   // page offsets are 32-bit buffer offsets
   if ((int64_t)block_size * num_kv_heads * head_dim > 0x7FFFFFFFLL) return MSKV_EUNSUPPORTED;
@@ -584,7 +591,7 @@ extern "C" int mskv_fp8_decode_attention(
       mskv_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, num_splits);
   if (need > 0 && (!workspace || workspace_bytes < need)) return MSKV_EWORKSPACE;
 
-  mskv::DecodeArgs a;
+  DecodeArgs a;
   a.q = (const uint16_t*)query;
   a.kc = (const uint8_t*)k_cache;
   a.vc = (const uint8_t*)v_cache;
@@ -599,15 +606,83 @@ extern "C" int mskv_fp8_decode_attention(
   a.hq = num_q_heads;
   a.hk = num_kv_heads;
   a.group = group;
-  a.qgroups = mskv::qgroups_of(group);
+  a.qgroups = qgroups_of(group);
   a.bs = block_size;
   a.w = max_blocks_per_seq;
   a.splits = num_splits;
-  a.pages_per_split = mskv::pages_per_split_of(num_splits, max_blocks_per_seq);
+  a.pages_per_split = pages_per_split_of(num_splits, max_blocks_per_seq);
   a.num_blocks = num_blocks;
-  a.scale_log2 = softmax_scale * mskv::kLog2e;
+  a.scale_log2 = softmax_scale * kLog2e;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e = act_dtype == MSKV_BFLOAT16 ? mskv::launch_decode<__bf16>(a, batch, s)
-                                            : mskv::launch_decode<_Float16>(a, batch, s);
+  hipError_t e = act_dtype == MSKV_BFLOAT16 ? launch_decode<__bf16>(a, batch, s)
+                                            : launch_decode<_Float16>(a, batch, s);
   return (int)e;
+}
+
+// The split-partials scratch of mskv_fp8_decode_attention_noalloc: a
+// file-scope device array, one copy per GPU, alive until the process ends.
+// Host code never uses its name as an address (on the host that is a
+// stand-in symbol, not device memory): each device's address comes from
+// hipGetSymbolAddress, looked up once per device with it current.
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// This device's address of `scratch`, looked up on its first use.
+static hipError_t scratch_for_current_device(void** ptr) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (p == nullptr) return hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return hipSuccess;
+}
+
+}  // namespace mskv
+
+extern "C" int mskv_fp8_decode_attention(
+    const void* query, const void* k_cache, const void* v_cache,
+    const float* k_scale_cache, const float* v_scale_cache,
+    const int32_t* cache_seqlens, const int32_t* block_tables, void* out,
+    int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+    int64_t num_blocks, int max_blocks_per_seq, float softmax_scale,
+    int act_dtype, int num_splits, void* workspace, size_t workspace_bytes,
+    void* stream) {
+  return mskv::decode_checked(query, k_cache, v_cache, k_scale_cache, v_scale_cache,
+                              cache_seqlens, block_tables, out, batch, num_q_heads,
+                              num_kv_heads, head_dim, block_size, num_blocks,
+                              max_blocks_per_seq, softmax_scale, act_dtype, num_splits,
+                              workspace, workspace_bytes, stream);
+}
+
+extern "C" int mskv_fp8_decode_attention_noalloc(
+    const void* query, const void* k_cache, const void* v_cache,
+    const float* k_scale_cache, const float* v_scale_cache,
+    const int32_t* cache_seqlens, const int32_t* block_tables, void* out,
+    int batch, int num_q_heads, int num_kv_heads, int head_dim, int block_size,
+    int64_t num_blocks, int max_blocks_per_seq, float softmax_scale,
+    int act_dtype, int num_splits, void* stream) {
+  const size_t need = mskv_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim,
+                                                  num_splits);
+  if (need > mskv::kNoAllocScratchBytes) return MSKV_EWORKSPACE;
+  void* ws = nullptr;
+  if (need > 0 && batch > 0) {
+    const hipError_t e = mskv::scratch_for_current_device(&ws);
+    if (e != hipSuccess) return (int)e;
+  }
+  return mskv::decode_checked(query, k_cache, v_cache, k_scale_cache, v_scale_cache,
+                              cache_seqlens, block_tables, out, batch, num_q_heads,
+                              num_kv_heads, head_dim, block_size, num_blocks,
+                              max_blocks_per_seq, softmax_scale, act_dtype, num_splits, ws,
+                              need, stream);
 }
