@@ -21,10 +21,11 @@
 //  * The S^T accumulator leaves lane (g, n) holding tokens {4g+r, 16+4g+r}
 //    of head n -- exactly the B-operand layout of O^T = V^T . P^T, so the
 //    probabilities never move between lanes.  P is scaled by the per-token
-//    v_scale and rounded to bf16 (fp32 range) for the PV MFMA.
+//    v_scale and a per-wave power of two and rounded to fp16 for the PV
+//    MFMA (11 significant bits; the power of two keeps fp16's range).
 //  * V^T's A operand needs eight tokens per lane at one d: it comes back
 //    out of the V tile transposed with ds_read_b64_tr_b8, then is converted
-//    fp8 -> bf16 in registers.
+//    fp8 -> fp16 (exact) in registers.
 //  * Tile rows are stored with their 16-byte chunks XOR-swizzled by
 //    (row / 2) % 8, which keeps the row-major writes and the K reads free
 //    of LDS bank conflicts; the transposed V reads are 2-way (rows r and
@@ -55,6 +56,9 @@
 namespace mskv {
 
 constexpr int kStep = 32;  // tokens per inner step (one LDS K/V tile pair)
+// p * v_scale is scaled so the largest v_scale maps to at most this: with
+// p < 2^8 every weight stays below 2^15, inside fp16's range
+constexpr float kPvScaleMax = 128.0f;
 constexpr int kMaxPagesPerSplit = 4;
 // Split-KV aims at this many waves: eight per CU
 constexpr int kTargetWaves = 2048;
@@ -63,7 +67,7 @@ constexpr int kTargetWaves = 2048;
 // with each other.
 constexpr int kWavesPerWG = 8;
 constexpr int kNarrowWaves = 4;       // workgroup shape for grids of many rounds
-constexpr int64_t kWideGridMax = 512; // 8-wave workgroups: two per CU of 256
+constexpr int64_t kWideGridMax = 512; // 8-wave workgroups: about two rounds
 // Largest split-partials scratch the allocation-free entry point serves
 constexpr size_t kNoAllocScratchBytes = MSKV_DECODE_NOALLOC_SCRATCH_BYTES;
 
@@ -125,46 +129,20 @@ __device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
   s.valid = ok ? min(kStep, t_end - t0) : 0;
 }
 
-// 3 waves per SIMD: the register budget (<= 168 VGPRs) that holds a whole
-// step in flight without spilling
-template <typename T, int W>
-__global__ __launch_bounds__(64 * W)
-__attribute__((amdgpu_waves_per_eu(3, 8)))
-void decode_fp8_kernel(DecodeArgs a) {
+// One wave's online softmax over the token range [t_begin, t_end) of
+// sequence b for kv head kvh (q head qh of the lane's column): returns the
+// un-normalized accumulator O^T, the running max m (log2 units) and the
+// lane's share of the denominator l.  kv_lds / s_lds are this wave's own
+// double-buffered LDS tiles.
+template <typename T>
+__device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int kvh, int qh,
+                                             bool head_ok, int t_begin, int t_end, int lane,
+                                             uint8_t (&kv_lds)[2][2][kStep * kHeadDim],
+                                             float (&s_lds)[2][2 * kStep], f32x4 (&acc)[8],
+                                             float& m, float& l) {
   using A = Act<T>;
   using x8 = typename A::x8;
-  // per wave: two K/V tile pairs and their scales; step i is read from
-  // buffer i&1 while step i+1 is staged into the other one
-  __shared__ __attribute__((aligned(16))) uint8_t kv_lds_all[W][2][2][kStep * kHeadDim];
-  __shared__ __attribute__((aligned(16))) float s_lds_all[W][2][2 * kStep];
-
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
   const int g = lane >> 4, n = lane & 15;
-  const int unit = blockIdx.x * W + wave, split = blockIdx.y, b = blockIdx.z;
-  if (unit >= a.hk * a.qgroups) return;
-  auto& kv_lds = kv_lds_all[wave];
-  auto& s_lds = s_lds_all[wave];
-  const int kvh = unit / a.qgroups;
-  const int hig = (unit - kvh * a.qgroups) * 16 + n;  // head within its group
-  const bool head_ok = hig < a.group;
-  const int qh = kvh * a.group + hig;
-  // tokens past the block table's width are not addressable: ignore them
-  const int L = min(a.seqlens[b], a.w * a.bs);
-  const int split_tokens = a.pages_per_split * a.bs;
-  const int t_begin = split * split_tokens;
-
-  if (L <= 0) {
-    if (a.splits == 1 && split == 0 && head_ok) {
-      uint16_t* op = a.out + ((int64_t)b * a.hq + qh) * kHeadDim;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt)
-        *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{0u, 0u};
-    }
-    return;
-  }
-  if (t_begin >= L) return;
-  const int t_end = min(L, t_begin + split_tokens);
 
   // Q^T as the B operand: lane (g, n) holds head n at d in
   // [16g, 16g+16) and [64+16g, 64+16g+16), eight per MFMA k-step.
@@ -181,10 +159,16 @@ void decode_fp8_kernel(DecodeArgs a) {
     for (int j = 0; j < 4; ++j) qop[j] = __builtin_bit_cast(x8, u32x4{0u, 0u, 0u, 0u});
   }
 
-  f32x4 acc[8];
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.0f;
+  m = -INFINITY;
+  l = 0.0f;
+  // The PV operand is fp16(p * v_scale * f): f is a power of two with
+  // v_scale * f <= kPvScaleMax for every valid token seen so far, so every
+  // weight stays within fp16's range (p < 2^8 under the lazy rescale) and
+  // fp16 keeps 11 significant bits; acc is in units of f, rescaled exactly
+  // when f shrinks.
+  float f = 0.0f, vseen = 0.0f;
 
   // ds_read_b64_tr_b8: in each 16-lane group, result byte e of lane i comes
   // from the address supplied by lane 2e + i/8, plus i%8.  Lane i therefore
@@ -197,7 +181,12 @@ void decode_fp8_kernel(DecodeArgs a) {
 
   // Stage one step's K/V rows and scales into LDS buffer `buf`.  V rows
   // past the sequence end are zeroed (their P is 0, and a stray NaN byte
-  // would otherwise poison the MFMA sum); their K scores are masked.
+  // would otherwise poison the MFMA sum); their K scores are masked.  The
+  // scales are stored premultiplied: k_scale * softmax_scale * log2(e),
+  // and v_scale * f after f has taken in this step's valid tokens (the
+  // accumulator holds the previous steps, so it is rescaled here).  A
+  // NaN v_scale (never stored by the store kernel) counts as out of range
+  // and is excluded from f by the max.
   auto stage = [&](const StepLoads& s, int buf) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -207,7 +196,23 @@ void decode_fp8_kernel(DecodeArgs a) {
       *reinterpret_cast<u32x4*>(&kv_lds[buf][1][o]) =
           row < s.valid ? s.v[c] : u32x4{0u, 0u, 0u, 0u};
     }
-    s_lds[buf][lane] = lane < 32 ? s.kscale : s.vscale;
+    const bool vtok = lane >= 32 && lane - 32 < s.valid;
+    if (__any(vtok && !(s.vscale * f <= kPvScaleMax)) || f == 0.0f) {
+      // first step, or a valid token whose weight could leave fp16's range:
+      // f from the largest v_scale of the step's valid tokens (and those
+      // before it), never growing
+      float vm = vtok ? s.vscale : 0.0f;
+      vm = fmaxf(max_xor32(max_xor16(max16_dpp(vm))), vseen);
+      const float fnew = vm > 0.0f ? pow2_floor(kPvScaleMax / vm) : 1.0f;
+      if (f != 0.0f && fnew < f) {
+        const float r = fnew / f;  // a power of two < 1: exact
+#pragma unroll
+        for (int dt = 0; dt < 8; ++dt) acc[dt] *= r;
+      }
+      if (f == 0.0f || fnew < f) f = fnew;
+      vseen = vm;
+    }
+    s_lds[buf][lane] = lane < 32 ? s.kscale * a.scale_log2 : s.vscale * f;
   };
   // K operand reads: token n (and 16 + n), chunks g and 4 + g
   const uint32_t k_lo = tile_off(n, g), k_hi = tile_off(n, 4 + g);
@@ -248,14 +253,14 @@ void decode_fp8_kernel(DecodeArgs a) {
     if (valid == kStep) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        x[r] = s0[r] * ksc0[r] * a.scale_log2;
-        x[4 + r] = s1[r] * ksc1[r] * a.scale_log2;
+        x[r] = s0[r] * ksc0[r];
+        x[4 + r] = s1[r] * ksc1[r];
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        x[r] = (4 * g + r < valid) ? s0[r] * ksc0[r] * a.scale_log2 : -INFINITY;
-        x[4 + r] = (16 + 4 * g + r < valid) ? s1[r] * ksc1[r] * a.scale_log2 : -INFINITY;
+        x[r] = (4 * g + r < valid) ? s0[r] * ksc0[r] : -INFINITY;
+        x[4 + r] = (16 + 4 * g + r < valid) ? s1[r] * ksc1[r] : -INFINITY;
       }
     }
     float tmax = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])),
@@ -272,18 +277,18 @@ void decode_fp8_kernel(DecodeArgs a) {
     }
     const float m_use = m == -INFINITY ? 0.0f : m;
     float psum = 0.0f;
-    bf16x8 pt;
+    f16x8 pt;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float p = exp2_fast(x[e] - m_use);
       psum += p;
-      const float vsc = e < 4 ? vsc0[e] : vsc1[e - 4];
-      pt[e] = (__bf16)(p * vsc);
+      const float vsc = e < 4 ? vsc0[e] : vsc1[e - 4];  // v_scale * f
+      pt[e] = (_Float16)(p * vsc);
     }
     if (valid != kStep) {
 #pragma unroll
       for (int e = 0; e < 8; ++e)
-        if (x[e] == -INFINITY) pt[e] = (__bf16)0.0f;
+        if (x[e] == -INFINITY) pt[e] = (_Float16)0.0f;
     }
     l += psum;
 
@@ -295,8 +300,8 @@ void decode_fp8_kernel(DecodeArgs a) {
           reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
               (__attribute__((address_space(3))) uint8_t*)vb + tr_base +
               ((16u * dt) ^ tr_swz)));
-      const bf16x8 vt = fp8x8_to_bf16((uint32_t)raw[0], (uint32_t)raw[1]);
-      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vt, pt, acc[dt], 0, 0, 0);
+      const f16x8 vt = fp8x8_to_f16((uint32_t)raw[0], (uint32_t)raw[1]);
+      acc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vt, pt, acc[dt], 0, 0, 0);
     }
     if (more) {
       stage(nxt, buf ^ 1);
@@ -304,34 +309,92 @@ void decode_fp8_kernel(DecodeArgs a) {
     }
     wave_lds_sync();
   }
-
   l = sum_xor32(sum_xor16(l));
-  uint16_t* op = a.out + ((int64_t)b * a.hq + qh) * kHeadDim;
-  // splits that hold tokens of this sequence; a sequence that fits in one
-  // split is written here directly
-  const int nvalid = min(a.splits, (L + split_tokens - 1) / split_tokens);
-  if (nvalid == 1) {
-    if (!head_ok) return;
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  if (f != 0.0f) {
+    const float inv_f = 1.0f / f;  // a power of two: exact
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const f32x4 o = acc[dt] * inv;
-      const uint32_t lo = (uint32_t)A::from_f32(o[0]) | ((uint32_t)A::from_f32(o[1]) << 16);
-      const uint32_t hi = (uint32_t)A::from_f32(o[2]) | ((uint32_t)A::from_f32(o[3]) << 16);
-      *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{lo, hi};
-    }
-    return;
+    for (int dt = 0; dt < 8; ++dt) acc[dt] *= inv_f;
   }
+}
 
-  // this split's partial: o / l and m + log2 l, merged by decode_combine_kernel
-  if (!head_ok) return;
-  const int64_t row = ((int64_t)b * a.hq + qh) * a.splits + split;
+// out[b, qh, :] = acc / l in the activation type (zeros when l == 0)
+template <typename T>
+__device__ __forceinline__ void write_output(uint16_t* op, const f32x4 (&acc)[8], float l,
+                                             int g) {
+  using A = Act<T>;
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  float* po = a.part_o + row * kHeadDim;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) {
+    const f32x4 o = acc[dt] * inv;
+    const uint32_t lo = (uint32_t)A::from_f32(o[0]) | ((uint32_t)A::from_f32(o[1]) << 16);
+    const uint32_t hi = (uint32_t)A::from_f32(o[2]) | ((uint32_t)A::from_f32(o[3]) << 16);
+    *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{lo, hi};
+  }
+}
+
+// a split's partial: o / l and m + log2 l (-inf when it saw no token)
+__device__ __forceinline__ void write_partial(float* po, float* plse, const f32x4 (&acc)[8],
+                                              float m, float l, int g) {
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt)
     *reinterpret_cast<f32x4*>(po + 16 * dt + 4 * g) = acc[dt] * inv;
-  if (g == 0) a.part_lse[row] = l > 0.0f ? m + __log2f(l) : -INFINITY;
+  if (g == 0) *plse = l > 0.0f ? m + __log2f(l) : -INFINITY;
+}
+
+// 3 waves per SIMD: the register budget (<= 168 VGPRs) that holds a whole
+// step in flight without spilling
+template <typename T, int W>
+__global__ __launch_bounds__(64 * W)
+__attribute__((amdgpu_waves_per_eu(3, 8)))
+void decode_fp8_kernel(DecodeArgs a) {
+  // per wave: two K/V tile pairs and their scales; step i is read from
+  // buffer i&1 while step i+1 is staged into the other one
+  __shared__ __attribute__((aligned(16))) uint8_t kv_lds_all[W][2][2][kStep * kHeadDim];
+  __shared__ __attribute__((aligned(16))) float s_lds_all[W][2][2 * kStep];
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int g = lane >> 4, n = lane & 15;
+  const int unit = blockIdx.x * W + wave, split = blockIdx.y, b = blockIdx.z;
+  if (unit >= a.hk * a.qgroups) return;
+  const int kvh = unit / a.qgroups;
+  const int hig = (unit - kvh * a.qgroups) * 16 + n;  // head within its group
+  const bool head_ok = hig < a.group;
+  const int qh = kvh * a.group + hig;
+  // tokens past the block table's width are not addressable: ignore them
+  const int L = min(a.seqlens[b], a.w * a.bs);
+  const int split_tokens = a.pages_per_split * a.bs;
+  const int t_begin = split * split_tokens;
+
+  if (L <= 0) {
+    if (a.splits == 1 && split == 0 && head_ok) {
+      uint16_t* op = a.out + ((int64_t)b * a.hq + qh) * kHeadDim;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt)
+        *reinterpret_cast<u32x2*>(op + 16 * dt + 4 * g) = u32x2{0u, 0u};
+    }
+    return;
+  }
+  if (t_begin >= L) return;
+  const int t_end = min(L, t_begin + split_tokens);
+
+  f32x4 acc[8];
+  float m, l;
+  attend_range<T>(a, b, kvh, qh, head_ok, t_begin, t_end, lane, kv_lds_all[wave],
+                  s_lds_all[wave], acc, m, l);
+
+  // splits that hold tokens of this sequence; a sequence that fits in one
+  // split is written here directly
+  const int nvalid = min(a.splits, (L + split_tokens - 1) / split_tokens);
+  if (!head_ok) return;
+  if (nvalid == 1) {
+    write_output<T>(a.out + ((int64_t)b * a.hq + qh) * kHeadDim, acc, l, g);
+    return;
+  }
+  // this split's partial, merged by a combine kernel
+  const int64_t row = ((int64_t)b * a.hq + qh) * a.splits + split;
+  write_partial(a.part_o + row * kHeadDim, a.part_lse + row, acc, m, l, g);
 }
 
 // out[b, h, :] = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M) over the
@@ -488,11 +551,10 @@ __global__ __launch_bounds__(64 * kWideWaves) void decode_combine_wide_kernel(
 static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
 
 template <typename T>
-static hipError_t launch_decode(const DecodeArgs& a, int batch,
-                                hipStream_t stream) {
-  // One 8-wave workgroup (128 KB of LDS) fills a CU.  While the grid of
-  // those is at most two per CU, they run as one even wave; a larger grid
-  // runs in rounds, and its tail shrinks with 4-wave workgroups (two per
+static hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream) {
+  // One 8-wave workgroup (128 KB of LDS) fills a CU.  A grid of at most
+  // kWideGridMax of those runs in about two rounds; a larger grid runs in
+  // many, and the last round's tail halves with 4-wave workgroups (two per
   // CU): ragged batch 256, 452 against 491 us; the Qwen3-8B batch 64 x 4096
   // step prefers 8 waves, 88.3 against 90.5 us.  Shapes only, so the choice
   // is the same on every call of a captured graph.

@@ -121,6 +121,19 @@ __device__ __forceinline__ bf16x8 fp8x8_to_bf16(uint32_t w0, uint32_t w1) {
   return r;
 }
 
+// eight e4m3fn bytes (two dwords) -> eight exact fp16 values
+__device__ __forceinline__ f16x8 fp8x8_to_f16(uint32_t w0, uint32_t w1) {
+  f16x8 r;
+  Act<_Float16>::fp8x4_to(w0, r, 0);
+  Act<_Float16>::fp8x4_to(w1, r, 4);
+  return r;
+}
+
+// largest power of two <= x, for a positive normal x
+__device__ __forceinline__ float pow2_floor(float x) {
+  return __uint_as_float(__float_as_uint(x) & 0xFF800000u);
+}
+
 // Four fp32 values -> four e4m3fn bytes (RNE, sign kept on zero).  The inputs
 // must already lie in [-448, 448].
 __device__ __forceinline__ uint32_t pack_fp8x4(float a, float b, float c,
@@ -177,6 +190,22 @@ __device__ __forceinline__ float max_xor32(float v) {
                                                   false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// max over each row of 16 lanes with DPP (no LDS round trip): quad_perm
+// [1,0,3,2] and [2,3,0,1] reduce each quad, row_half_mirror pairs lane i
+// with 7-i (the other quad of its half-row), row_mirror lane i with 15-i
+// (the other half-row)
+__device__ __forceinline__ float max16_dpp(float v) {
+  int x = __float_as_int(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0xB1, 0xF, 0xF, false)));
+  x = __float_as_int(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x4E, 0xF, 0xF, false)));
+  x = __float_as_int(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x141, 0xF, 0xF, false)));
+  x = __float_as_int(v);
+  v = fmaxf(v, __int_as_float(__builtin_amdgcn_update_dpp(x, x, 0x140, 0xF, 0xF, false)));
+  return v;
+}
+
 __device__ __forceinline__ float sum_xor16(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v),
                                                   false, false);

@@ -106,11 +106,6 @@ __device__ __forceinline__ f32x4 mfma_fp8_scale_b(const i32x8& a, const i32x8& b
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, sb);
 }
 
-// largest power of two <= x, for a positive normal x
-__device__ __forceinline__ float pow2_floor(float x) {
-  return __uint_as_float(__float_as_uint(x) & 0xFF800000u);
-}
-
 // Direct global -> LDS loads (buffer_load ... lds): lane i of the wave
 // writes its `bytes` at lds + i * bytes, from any per-lane offset.
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
