@@ -154,9 +154,10 @@ int mskv_fp8_decode_attention_noalloc(const void* query, const void* k_cache,
  * p < (Lk - Lq) + i + 1 (fp8_chunk_prefill_attention.py:52-54).
  * When cu_seqlens_q and cu_seqlens_k are both NULL the batch is one
  * sequence of total_q queries over prefix_len + total_q positions, exactly
- * the reference's signature.  QK^T and PV run as FP8 MFMA contractions: the
- * query is split into e4m3 parts under a power-of-two row scale, and the
- * probabilities into hi + lo parts under a per-row E8M0 block scale.
+ * the reference's signature.  QK^T runs as FP8 MFMA contractions, the
+ * query split into e4m3 parts under a power-of-two row scale; PV runs on
+ * the fp16 MFMA with V converted exactly and weights p * v_scale rounded to
+ * fp16 under a power-of-two scale.
  * query/out: [total_q, num_q_heads, head_dim] in act_dtype; block_tables:
  * int32 [num_seqs, max_blocks_per_seq].  max_seqlen_q must be at least
  * every sequence's query count: it sizes the grid, and query rows past it

@@ -10,10 +10,8 @@
 //  * A workgroup covers 128 rows of one (sequence, kv head, block of query
 //    tokens).  A row is one (query token, q head) pair; the GQA group of the
 //    kv head fills the rows, so every K/V tile serves all the q heads that
-//    read it.  Four waves of two 16-row blocks, so every K operand a wave
-//    reads from LDS feeds both.  bf16 also shares each V^T operand between
-//    the blocks; fp16, whose query needs a third e4m3 part, computes one
-//    block's P and PV at a time to stay within the register file.
+//    read it.  Four waves of two 16-row blocks, so every K and V^T operand a
+//    wave reads from LDS (and converts) feeds both.
 //  * K/V tiles of 128 keys (one f8f6f4 MFMA contraction) are staged in LDS,
 //    double-buffered with one barrier per tile.  Rows are written with their
 //    16-byte chunks XOR-swizzled by (row / 2) % 8, which keeps the row
@@ -25,17 +23,15 @@
 //    scaled by a power of two (exact) and split into e4m3 parts: hi + lo
 //    represent a bf16 query exactly (4 + 4 significant bits), fp16 needs
 //    hi + mid + lo; one MFMA per part into the same accumulator.
-//  * PV: O^T = V^T . P8^T with the same MFMA.  S^T's accumulator leaves lane
-//    (g, n) holding 32 keys of row n, exactly the B-operand layout of P^T,
-//    so probabilities never move between lanes; V^T comes out of LDS with
-//    ds_read_b64_tr_b8.  P * v_scale is split into e4m3 hi + lo parts after
-//    a per-tile power-of-two scale chosen from the tile's largest v_scale;
-//    the accumulator is rescaled (exactly) only when that power changes.
-//  * The softmax denominator sums the weights the MFMA applies,
-//    (hi + lo) / v_scale, so each output is an exact convex combination of
-//    V rows.  Each wave computes the tile's 1 / v_scale once per key into
-//    LDS; keys whose V is too small for their weights to fit e4m3 add their
-//    exact p on a rare wave-uniform path instead.
+//  * PV: O^T = V^T . P^T with v_mfma_f32_16x16x32_f16, which runs at the
+//    same rate per key as two FP8 parts would.  S^T's accumulator leaves
+//    lane (g, n) holding 32 keys of row n, exactly the B-operand layout of
+//    P^T, so probabilities never move between lanes; V^T comes out of LDS
+//    with ds_read_b64_tr_b8 and converts to fp16 exactly.  Each weight is
+//    fp16(p * v_scale * fw), fw a per-wave power of two set from the largest
+//    v_scale seen, so the weights keep 11 significant bits whatever the
+//    spread of v_scale inside a tile.  The softmax denominator sums p * fw
+//    in fp32.
 //  * Online softmax in base 2 with a lazy rescale: the accumulator is
 //    rescaled only when some row's max grows by more than 2^8.  Masks are
 //    evaluated only on tiles that straddle the causal diagonal or the end
@@ -52,30 +48,22 @@
 namespace mskv {
 
 constexpr int kPStep = 128;  // keys per tile
-// A workgroup covers 128 rows: 4 waves of two 16-row blocks.  fp16's third
-// query part costs 16 registers, which it wins back by running the P and
-// PV work of its two blocks one after the other.
-template <int NQ> struct PShape {
+// A workgroup covers 128 rows: 4 waves of two 16-row blocks.
+struct PShape {
   static constexpr int blocks = 2;  // 16-row blocks per wave
   static constexpr int waves = 8 / blocks;
   static constexpr int threads = 64 * waves;
 };
 // The running max may lag a row's true max by up to kPSlack (log2 units)
-// before the accumulator is rescaled.  P is normalized per row and tile
-// (see below), so the slack does not cost P precision.
+// before the accumulator is rescaled, so p stays below 2^8.
 constexpr float kPSlack = 8.0f;
-// The tile's v_scales are scaled by a power of two to at most this value, so
-// p * v_scale (p <= 1 after the per-row normalization) stays within 448.
-constexpr float kPVScaleMax = 384.0f;
-// Below this v_scale * fcur the two e4m3 parts of a key's weight
-// p * v_scale * fcur (at most 1/4 for such a key) hold too few bits for
-// its share of the softmax denominator, so its exact p goes there instead.
-constexpr float kPTinyV = 0.25f;
+// Largest v_scale * fw: a weight p * v_scale * fw with p <= 2^8 then stays
+// below 2^15, inside fp16's range.
+constexpr float kPVScaleMax = 128.0f;
 
 // e4m3 parts the query is split into: a bf16 value has 8 significant bits
 template <typename T> struct QuerySplit { static constexpr int parts = 3; };
 template <> struct QuerySplit<__bf16> { static constexpr int parts = 2; };
-template <typename T> using PShapeOf = PShape<QuerySplit<T>::parts>;
 
 struct PrefillArgs {
   const uint16_t* q;
@@ -99,13 +87,6 @@ __device__ __forceinline__ f32x4 mfma_fp8(const i32x8& a, const i32x8& b, f32x4 
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
-// The same MFMA with an E8M0 block scale on B: lane (g, n)'s scale byte sb
-// multiplies its column n, k-block g by 2^(sb - 127) (A's scale is 1.0).
-__device__ __forceinline__ f32x4 mfma_fp8_scale_b(const i32x8& a, const i32x8& b, f32x4 c,
-                                                  int sb) {
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, sb);
-}
-
 // Direct global -> LDS loads (buffer_load ... lds): lane i of the wave
 // writes its `bytes` at lds + i * bytes, from any per-lane offset.
 __device__ __forceinline__ void lds_load16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t off) {
@@ -118,11 +99,11 @@ __device__ __forceinline__ void lds_load4(__amdgpu_buffer_rsrc_t r, void* lds, u
 }
 
 template <typename T>
-__global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(PrefillArgs a) {
   using A = Act<T>;
   constexpr int NQ = QuerySplit<T>::parts;
-  constexpr int kPBlocks = PShapeOf<T>::blocks;
-  constexpr int kPWaves = PShapeOf<T>::waves;
+  constexpr int kPBlocks = PShape::blocks;
+  constexpr int kPWaves = PShape::waves;
   // two tile buffers as separate objects, and a loop unrolled by two, so
   // the compiler can see that the direct loads into one buffer never alias
   // the reads of the other (otherwise it waits for them before every read)
@@ -132,8 +113,6 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
   __shared__ __attribute__((aligned(16))) uint8_t v_lds1[kPStep * kHeadDim];
   __shared__ __attribute__((aligned(16))) float sc_lds0[2][kPStep];
   __shared__ __attribute__((aligned(16))) float sc_lds1[2][kPStep];
-  // each wave's reciprocals of the current tile's v_scales
-  __shared__ __attribute__((aligned(16))) float rv_lds[kPWaves][kPStep];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -236,9 +215,10 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
     m[b] = -INFINITY;
     l[b] = 0.0f;
   }
-  // acc and l are kept in units of fcur, the power-of-two scale applied to
-  // p * v_scale; lf = log2(fcur) is folded into the exp argument
-  float fcur = 1.0f, lf = 0.0f;
+  // acc and l are kept in units of fw, the power-of-two scale applied to
+  // p * v_scale (0 until the first tile with a stored token sets it);
+  // lf = log2(fw) is folded into the exp argument
+  float fw = 0.0f, lf = 0.0f;
 
   // K operand: key n of each 16-key group, 16-byte chunks 2g and 2g + 1;
   // the swizzle of rows 16t + n does not depend on t
@@ -374,190 +354,70 @@ __global__ __launch_bounds__(PShapeOf<T>::threads, 2) void prefill_fp8_kernel(Pr
           m[b] = m_new;
         }
       }
-      // this tile's power-of-two scale for p * v_scale, from its largest
-      // v_scale (lane group g reads keys 16tt + 4g + r)
-      float vm = 0.0f;
+      // The PV product runs on v_mfma_f32_16x16x32_f16.  V converts to fp16
+      // exactly, and each weight is fp16(p * v_scale * fw), 11 significant
+      // bits.  fw is a power of two per wave, set from the largest v_scale
+      // the wave has seen: v_scale * fw <= kPVScaleMax, so with p <= 2^8
+      // (the lazy rescale's slack) no weight leaves fp16's range.  It only
+      // ever shrinks, and the accumulator and l are then rescaled by the
+      // exact ratio.  log2(fw) is folded into the exp argument, so exp2
+      // returns p * fw, which l sums in fp32.
+      {
+        float vm = fmaxf(vss[lane], vss[64 + lane]);
+        vm = max_xor32(max_xor16(max16_dpp(vm)));
+        if (vm > 0.0f && (fw == 0.0f || vm * fw > kPVScaleMax)) {
+          const float fnew = pow2_floor(kPVScaleMax / vm);
+          if (fw != 0.0f) {
+            const float r = fnew / fw;  // a power of two: exact
 #pragma unroll
-      for (int tt = 0; tt < 8; ++tt) {
-        const f32x4 v4 = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
-        vm = fmaxf(vm, fmaxf(fmaxf(v4[0], v4[1]), fmaxf(v4[2], v4[3])));
-      }
-      vm = max_xor32(max_xor16(vm));
-      if (vm > 0.0f) {
-        const float ft = pow2_floor(kPVScaleMax / vm);
-        if (ft != fcur) {
-          const float r = ft / fcur;  // a power of two: exact
+            for (int b = 0; b < kPBlocks; ++b) {
+              l[b] *= r;
 #pragma unroll
-          for (int b = 0; b < kPBlocks; ++b) {
-            l[b] *= r;
-#pragma unroll
-            for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= r;
+              for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= r;
+            }
           }
-          fcur = ft;
-          lf = (float)((int)((__float_as_uint(ft) >> 23) & 0xFFu) - 127);
+          fw = fnew;
+          lf = (float)((int)((__float_as_uint(fnew) >> 23) & 0xFFu) - 127);
         }
       }
-      // P, normalized per row and tile: with k = floor(m - tile max) the row's
-      // largest p * 2^k is at most 1, so a tile far below the row max keeps
-      // its probabilities out of e4m3's underflow; the PV MFMA multiplies
-      // 2^-k back through its per-row E8M0 scale on P.
-      // y = p * 2^k * fcur * v_scale is split into e4m3 hi + lo.  l sums the
-      // weights the MFMA actually applies, (hi + lo) / v_scale * 2^-k, not p:
-      // the output is then an exact convex combination of V rows under those
-      // weights, so a row dominated by one key returns that key's V without
-      // the split's 2^-9 error.
-      i32x8 p8h[kPBlocks], p8l[kPBlocks];
-      float m_use[kPBlocks], lsum[kPBlocks];
-      int kr[kPBlocks];
+      float m_use[kPBlocks];
+#pragma unroll
+      for (int b = 0; b < kPBlocks; ++b) m_use[b] = (m[b] == -INFINITY ? 0.0f : m[b]) - lf;
+      // The wave raises its priority over the P loop and the PV MFMAs and
+      // drops it after.
+      __builtin_amdgcn_s_setprio(1);
+      // P^T for the f16 MFMA: 32-key chunk c of the tile is S^T tiles 2c and
+      // 2c + 1, so lane (g, n) holds keys 32c + 4g + r and 32c + 16 + 4g + r
+      // of row n -- the order in which ds_read_b64_tr_b8 hands it V^T
+      f16x8 pw[kPBlocks][4];
 #pragma unroll
       for (int b = 0; b < kPBlocks; ++b) {
-        const float kf =
-            tm[b] == -INFINITY ? 0.0f : fminf(floorf(m[b] - tm[b]), 127.0f);
-        kr[b] = (int)kf;
-        m_use[b] = (m[b] == -INFINITY ? 0.0f : m[b]) - lf - kf;
-        lsum[b] = 0.0f;
-      }
-      // 1 / v_scale of the tile's keys, computed once per key by this wave
-      // (lane i: keys i and 64 + i) instead of once per lane group, and read
-      // back below like the scales.  v_scale is 0 only for keys past
-      // `valid`, whose weights are 0.  The wave reads back only its own
-      // writes, so a wave-level barrier orders them.
-      // A key whose v_scale * fcur is below kPTinyV (V amax under ~1/1500 of
-      // the tile's largest, e.g. a V row stored as zeros) would get weights
-      // p * v_scale too small for e4m3 to carry, and its probability would
-      // drop out of l.  Its reciprocal is 0 instead, and its exact weight
-      // joins l on the rare path below.  Its V contribution stays with the
-      // MFMA, which it changes by at most p / 1500 of the tile's largest |V|.
-      float* rvw = rv_lds[wave];
-      bool tiny_keys;
-      {
-        const float v0 = vss[lane], v1 = vss[64 + lane];
-        const bool t0 = v0 > 0.0f && v0 * fcur < kPTinyV;
-        const bool t1 = v1 > 0.0f && v1 * fcur < kPTinyV;
-        rvw[lane] = v0 > 0.0f && !t0 ? __builtin_amdgcn_rcpf(v0) : 0.0f;
-        rvw[64 + lane] = v1 > 0.0f && !t1 ? __builtin_amdgcn_rcpf(v1) : 0.0f;
-        tiny_keys = __any(t0 || t1);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      }
-      if (tiny_keys) {
+        float psum = 0.0f;
 #pragma unroll
         for (int tt = 0; tt < 8; ++tt) {
           const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            if (vsc[r] > 0.0f && vsc[r] * fcur < kPTinyV) {
-#pragma unroll
-              for (int b = 0; b < kPBlocks; ++b) {
-                // opaque to the optimizer: shared with the loop below, these
-                // exps would be hoisted out of the loop's MFMA interleave
-                float x = fmaf(st[b][tt][r], qs[b], -m_use[b]);
-                asm volatile("" : "+v"(x));
-                lsum[b] += exp2_fast(x);
-              }
-            }
+            const float pf = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b]));
+            psum += pf;
+            pw[b][tt >> 1][4 * (tt & 1) + r] = (_Float16)(pf * vsc[r]);
           }
         }
+        l[b] += psum;
       }
-      typedef float f32x2 __attribute__((ext_vector_type(2)));
-      // The wave raises its priority over the P loop and the PV MFMAs and
-      // drops it after: bf16 1.9% and fp16 0.6% faster.
-      __builtin_amdgcn_s_setprio(1);
-      if constexpr (NQ == 3) {
-        // fp16: the third query part takes the registers of one block's P
-        // operands, so each block computes its P and runs its PV MFMAs in
-        // turn, reading V^T once per block
+      // O^T += V^T . P^T, one 16-wide d tile and 32-key chunk per MFMA
 #pragma unroll
-        for (int b = 0; b < kPBlocks; ++b) {
-          i32x8 ph, pl;
+      for (int dt = 0; dt < 8; ++dt) {
 #pragma unroll
-          for (int tt = 0; tt < 8; ++tt) {
-            const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
-            const f32x4 rv = *reinterpret_cast<const f32x4*>(rvw + 16 * tt + 4 * g);
-            float y[4];
+        for (int c = 0; c < 4; ++c) {
+          const i32x2 raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+              reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
+                  (__attribute__((address_space(3))) uint8_t*)vt + tr_row[c] +
+                  ((16u * dt) ^ tr_swz[c])));
+          const f16x8 va = fp8x8_to_f16((uint32_t)raw[0], (uint32_t)raw[1]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              y[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b])) * vsc[r];
-            const uint32_t h = pack_fp8x4(y[0], y[1], y[2], y[3]);
-            const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
-            const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
-            const uint32_t lo = pack_fp8x4(y[0] - h01[0], y[1] - h01[1], y[2] - h23[0],
-                                           y[3] - h23[1]);
-            const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
-            const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
-            lsum[b] = fmaf(h01[0] + l01[0], rv[0], lsum[b]);
-            lsum[b] = fmaf(h01[1] + l01[1], rv[1], lsum[b]);
-            lsum[b] = fmaf(h23[0] + l23[0], rv[2], lsum[b]);
-            lsum[b] = fmaf(h23[1] + l23[1], rv[3], lsum[b]);
-            ph[tt] = (int)h;
-            pl[tt] = (int)lo;
-          }
-          l[b] += __builtin_amdgcn_ldexpf(lsum[b], -kr[b]);
-#pragma unroll
-          for (int dt = 0; dt < 8; ++dt) {
-            i32x8 va;
-#pragma unroll
-            for (int qq = 0; qq < 4; ++qq) {
-              const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                  reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
-                      (__attribute__((address_space(3))) uint8_t*)vt + tr_row[qq] +
-                      ((16u * dt) ^ tr_swz[qq])));
-              va[2 * qq] = r[0];
-              va[2 * qq + 1] = r[1];
-            }
-            acc[b][dt] = mfma_fp8_scale_b(va, ph, acc[b][dt], 127 - kr[b]);
-            acc[b][dt] = mfma_fp8_scale_b(va, pl, acc[b][dt], 127 - kr[b]);
-          }
-          // keep the next block's P work out of this block's PV
-          __builtin_amdgcn_sched_barrier(0);
-        }
-      } else {
-  #pragma unroll
-        for (int tt = 0; tt < 8; ++tt) {
-          const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
-          const f32x4 rv = *reinterpret_cast<const f32x4*>(rvw + 16 * tt + 4 * g);
-  #pragma unroll
-          for (int b = 0; b < kPBlocks; ++b) {
-            float y[4];
-  #pragma unroll
-            for (int r = 0; r < 4; ++r)
-              y[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b])) * vsc[r];
-            const uint32_t h = pack_fp8x4(y[0], y[1], y[2], y[3]);
-            const f32x2 h01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, false);
-            const f32x2 h23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)h, true);
-            const uint32_t lo = pack_fp8x4(y[0] - h01[0], y[1] - h01[1], y[2] - h23[0],
-                                           y[3] - h23[1]);
-            const f32x2 l01 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, false);
-            const f32x2 l23 = __builtin_amdgcn_cvt_pk_f32_fp8((int)lo, true);
-            lsum[b] = fmaf(h01[0] + l01[0], rv[0], lsum[b]);
-            lsum[b] = fmaf(h01[1] + l01[1], rv[1], lsum[b]);
-            lsum[b] = fmaf(h23[0] + l23[0], rv[2], lsum[b]);
-            lsum[b] = fmaf(h23[1] + l23[1], rv[3], lsum[b]);
-            p8h[b][tt] = (int)h;
-            p8l[b][tt] = (int)lo;
-          }
-        }
-  #pragma unroll
-        for (int b = 0; b < kPBlocks; ++b) l[b] += __builtin_amdgcn_ldexpf(lsum[b], -kr[b]);
-        // O^T += V^T . P8^T, one 16-wide d tile per MFMA pair
-  #pragma unroll
-        for (int dt = 0; dt < 8; ++dt) {
-          i32x8 va;
-  #pragma unroll
-          for (int qq = 0; qq < 4; ++qq) {
-            const i32x2 r = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-                reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
-                    (__attribute__((address_space(3))) uint8_t*)vt + tr_row[qq] +
-                    ((16u * dt) ^ tr_swz[qq])));
-            va[2 * qq] = r[0];
-            va[2 * qq + 1] = r[1];
-          }
-  #pragma unroll
-          for (int b = 0; b < kPBlocks; ++b) {
-            acc[b][dt] = mfma_fp8_scale_b(va, p8h[b], acc[b][dt], 127 - kr[b]);
-            acc[b][dt] = mfma_fp8_scale_b(va, p8l[b], acc[b][dt], 127 - kr[b]);
-          }
+          for (int b = 0; b < kPBlocks; ++b)
+            acc[b][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pw[b][c], acc[b][dt], 0, 0, 0);
         }
       }
       __builtin_amdgcn_s_setprio(0);
@@ -661,9 +521,9 @@ extern "C" int mskv_fp8_prefill_attention(
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (act_dtype == MSKV_BFLOAT16)
     hipLaunchKernelGGL(mskv::prefill_fp8_kernel<__bf16>, grid,
-                       dim3(mskv::PShapeOf<__bf16>::threads), 0, s, a);
+                       dim3(mskv::PShape::threads), 0, s, a);
   else
     hipLaunchKernelGGL(mskv::prefill_fp8_kernel<_Float16>, grid,
-                       dim3(mskv::PShapeOf<_Float16>::threads), 0, s, a);
+                       dim3(mskv::PShape::threads), 0, s, a);
   return (int)hipGetLastError();
 }
