@@ -389,36 +389,55 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
       // P^T for the f16 MFMA: 32-key chunk c of the tile is S^T tiles 2c and
       // 2c + 1, so lane (g, n) holds keys 32c + 4g + r and 32c + 16 + 4g + r
       // of row n -- the order in which ds_read_b64_tr_b8 hands it V^T
+      // Each 16-key group's v_scales are read once for both blocks, one
+      // group ahead: read per block and group, every read's LDS latency was
+      // exposed.
       f16x8 pw[kPBlocks][4];
+      float psum[kPBlocks] = {};
+      f32x4 vsc_next = *reinterpret_cast<const f32x4*>(vss + 4 * g);
 #pragma unroll
-      for (int b = 0; b < kPBlocks; ++b) {
-        float psum = 0.0f;
+      for (int tt = 0; tt < 8; ++tt) {
+        const f32x4 vsc = vsc_next;
+        if (tt < 7) vsc_next = *reinterpret_cast<const f32x4*>(vss + 16 * (tt + 1) + 4 * g);
 #pragma unroll
-        for (int tt = 0; tt < 8; ++tt) {
-          const f32x4 vsc = *reinterpret_cast<const f32x4*>(vss + 16 * tt + 4 * g);
+        for (int b = 0; b < kPBlocks; ++b) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const float pf = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b]));
-            psum += pf;
+            psum[b] += pf;
             pw[b][tt >> 1][4 * (tt & 1) + r] = (_Float16)(pf * vsc[r]);
           }
         }
-        l[b] += psum;
       }
-      // O^T += V^T . P^T, one 16-wide d tile and 32-key chunk per MFMA
+#pragma unroll
+      for (int b = 0; b < kPBlocks; ++b) l[b] += psum[b];
+      // O^T += V^T . P^T, one 16-wide d tile and 32-key chunk per MFMA.  The
+      // V^T reads of d tile dt + 1 are issued before the MFMAs of tile dt:
+      // with one read in flight, each chunk's LDS latency sat behind only
+      // two 16-cycle MFMAs.
+      auto vread = [&](int dt, int c) {
+        return __builtin_amdgcn_ds_read_tr8_b64_v2i32(
+            reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
+                (__attribute__((address_space(3))) uint8_t*)vt + tr_row[c] +
+                ((16u * dt) ^ tr_swz[c])));
+      };
+      i32x2 raw[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) raw[c] = vread(0, c);
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) {
+        i32x2 nxt[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c) nxt[c] = vread(dt < 7 ? dt + 1 : dt, c);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
-          const i32x2 raw = __builtin_amdgcn_ds_read_tr8_b64_v2i32(
-              reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
-                  (__attribute__((address_space(3))) uint8_t*)vt + tr_row[c] +
-                  ((16u * dt) ^ tr_swz[c])));
-          const f16x8 va = fp8x8_to_f16((uint32_t)raw[0], (uint32_t)raw[1]);
+          const f16x8 va = fp8x8_to_f16((uint32_t)raw[c][0], (uint32_t)raw[c][1]);
 #pragma unroll
           for (int b = 0; b < kPBlocks; ++b)
             acc[b][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pw[b][c], acc[b][dt], 0, 0, 0);
         }
+#pragma unroll
+        for (int c = 0; c < 4; ++c) raw[c] = nxt[c];
       }
       __builtin_amdgcn_s_setprio(0);
     }
