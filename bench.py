@@ -223,8 +223,9 @@ def time_config1(dev, iters=200, warmup=20, cpu_budget_s=8.0, cpu=True):
            "us": round(us, 2), "tokens_stored": n, "bytes": st_bytes + dec_bytes,
            "gbs": round((st_bytes + dec_bytes) / us / 1e3, 1),
            "store_tokens_per_s": round(n / us * 1e6, 1),
-           "note": "a 32 MB pool: the step runs from the caches and is launch-latency bound, "
-                   "so GB/s here is not an HBM figure"}
+           "note": "a 32 MB pool: the step runs from the caches, so GB/s here is not an HBM "
+                   "figure; device time per step, the steps queued behind a spin kernel so "
+                   "that no host launch time is counted"}
     if not cpu:
         return res
     from oracle import fp8_oracle as O
@@ -327,14 +328,36 @@ def time_prefill(dev, iters=20, warmup=3, dtype=torch.bfloat16):
             "peak_tflops": FP8_PEAK_TFLOPS, "frac": round(tflops / FP8_PEAK_TFLOPS, 4)}
 
 
+_SPIN_CYCLES_PER_MS = None
+
+
+def _spin(ms):
+    """Keep the current stream busy for about `ms` milliseconds (torch's
+    clock-spin kernel, its rate measured once)."""
+    global _SPIN_CYCLES_PER_MS
+    if _SPIN_CYCLES_PER_MS is None:
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        torch.cuda._sleep(1_000_000)
+        e1.record()
+        torch.cuda.synchronize()
+        _SPIN_CYCLES_PER_MS = 1_000_000 / max(e0.elapsed_time(e1), 1e-3)
+    torch.cuda._sleep(int(_SPIN_CYCLES_PER_MS * ms))
+
+
 def _time_steps(step, iters, warmup):
-    """Average HIP-event time of step(i) on the current stream, in us."""
+    """Average device time of step(i) on the current stream, in us.  The
+    timed steps are queued behind a spin kernel long enough for the host to
+    enqueue all of them, so each event pair brackets the step's kernels and
+    the gaps between them, not the host's launch path (which is slower
+    than the GPU for steps of a few tens of microseconds)."""
     for i in range(warmup):
         step(i)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(iters)]
+    _spin(0.25 * iters + 5.0)
     for i, (e0, e1) in enumerate(evs):
         e0.record(stream)
         step(i)
