@@ -30,9 +30,9 @@
 //    group, lane i's element j comes from the address of lane 4j + i/4 plus
 //    2 * (i % 4) bytes.
 //  * P is rounded to the activation type for the PV MFMA (as flash-attn
-//    does) and l sums the rounded values (v_dot2 of each rounded pair with
-//    (1, 1)), so each output is an exact convex combination of V rows under
-//    the weights applied.
+//    does) and l sums the rounded values, as a ninth output tile of the PV
+//    product whose V^T operand is all ones, so each output is an exact
+//    convex combination of V rows under the weights applied.
 //  * Online softmax in base 2 with a lazy rescale (slack 2^8; p <= 256 fits
 //    both fp16 and bf16); masks only on tiles that straddle the diagonal or
 //    the end of the keys; query blocks launch last-first across the whole
@@ -52,22 +52,15 @@ constexpr int kDRow = 2 * kHeadDim;  // bytes per K/V row
 constexpr int kDTile = kDStep * kDRow;
 constexpr float kDSlack = 8.0f;
 
-// Two probabilities rounded to the activation type, and l += their rounded
-// sum in fp32 with one v_dot2_f32_{bf16,f16} against (1, 1).
+// Two probabilities rounded to the activation type.
 template <typename T> struct PPair;
 template <> struct PPair<__bf16> {
   typedef __bf16 t2 __attribute__((ext_vector_type(2)));
   __device__ static t2 pack(float a, float b) { return t2{(__bf16)a, (__bf16)b}; }
-  __device__ static float acc(t2 v, float l) {
-    return __builtin_amdgcn_fdot2_f32_bf16(v, t2{(__bf16)1.0f, (__bf16)1.0f}, l, false);
-  }
 };
 template <> struct PPair<_Float16> {
   typedef _Float16 t2 __attribute__((ext_vector_type(2)));
   __device__ static t2 pack(float a, float b) { return t2{(_Float16)a, (_Float16)b}; }
-  __device__ static float acc(t2 v, float l) {
-    return __builtin_amdgcn_fdot2(v, t2{(_Float16)1.0f, (_Float16)1.0f}, l, false);
-  }
 };
 
 struct DenseArgs {
@@ -154,14 +147,17 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
       qop[b][c] = __builtin_bit_cast(x8, row_ok[b] ? qp[4 * c] : u32x4{0u, 0u, 0u, 0u});
   }
 
-  f32x4 acc[kDBlocks][8];
-  float m[kDBlocks], l[kDBlocks];
+  // acc: O^T; lacc: the denominator, as a ninth output tile whose V^T
+  // operand is all ones, so each of its rows is the column's sum of the
+  // rounded probabilities
+  f32x4 acc[kDBlocks][8], lacc[kDBlocks];
+  float m[kDBlocks];
 #pragma unroll
   for (int b = 0; b < kDBlocks; ++b) {
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[b][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    lacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     m[b] = -INFINITY;
-    l[b] = 0.0f;
   }
 
   // K operand: key n of each 16-key group, chunk 4c + g; the row swizzle
@@ -240,7 +236,7 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
       for (int b = 0; b < kDBlocks; ++b) {
         const float m_new = fmaxf(m[b], tm[b]);
         const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[b] - m_new);
-        l[b] *= alpha;
+        lacc[b] *= alpha;
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= alpha;
         m[b] = m_new;
@@ -251,18 +247,15 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
 #pragma unroll
     for (int b = 0; b < kDBlocks; ++b) {
       const float m_use = m[b] == -INFINITY ? 0.0f : m[b];
-      float psum = 0.0f;
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; r += 2) {
           const auto pk = PPair<T>::pack(exp2_fast(fmaf(st[b][tt][r], a.scale_log2, -m_use)),
                                          exp2_fast(fmaf(st[b][tt][r + 1], a.scale_log2, -m_use)));
-          psum = PPair<T>::acc(pk, psum);
           pv[b][tt >> 1][4 * (tt & 1) + r] = pk[0];
           pv[b][tt >> 1][4 * (tt & 1) + r + 1] = pk[1];
         }
-      l[b] += psum;
     }
     // O^T += V^T . P^T, one 16-wide d tile and 32-key chunk per MFMA.  The
     // wave raises its priority over this loop (the probabilities' rounding
@@ -287,6 +280,18 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
 #pragma unroll
         for (int b = 0; b < kDBlocks; ++b) acc[b][dt] = A::mfma(va, pv[b][ch], acc[b][dt]);
       }
+    }
+    // the denominator: sums of the probabilities as rounded for the MFMA,
+    // so each output is an exact convex combination of V rows under them
+    // (a chain of v_dot2 per pair did the same at 4% of the kernel's time)
+    {
+      x8 ones;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ones[i] = (T)1.0f;
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int b = 0; b < kDBlocks; ++b) lacc[b] = A::mfma(ones, pv[b][ch], lacc[b]);
     }
     __builtin_amdgcn_s_setprio(0);
   };
@@ -314,7 +319,7 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
 
 #pragma unroll
   for (int b = 0; b < kDBlocks; ++b) {
-    const float lt = sum_xor32(sum_xor16(l[b]));
+    const float lt = lacc[b][0];
     if (!row_ok[b]) continue;
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     uint16_t* op =
