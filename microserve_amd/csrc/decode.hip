@@ -43,6 +43,11 @@
 //    agent-scope fences, i.e. an L2 writeback + invalidate per XCD, which
 //    measured 2x slower).  A sequence that fits in one split is written
 //    directly by the split kernel.
+//  * Two workgroup shapes, chosen from shapes alone: 8 waves (all 8 kv
+//    heads of a token range, whole 1 KiB token rows, 132 KB of LDS: one per
+//    CU) while the grid holds at most 512 of them, about two rounds; 4
+//    waves (half a token row each, two per CU) for larger grids, whose
+//    smaller last round halves the tail.
 //  * Every page is read through a buffer resource sized to that page; an
 //    invalid block id gives a zero-length resource (loads return 0) and its
 //    tokens are masked, so a bad table entry cannot fault.
