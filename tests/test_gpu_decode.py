@@ -186,6 +186,33 @@ def test_decode_narrow_workgroups_wide_gqa_group():
     _run_and_check(query, lens, tables, caches)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_decode_v_scale_growing_along_the_sequence(dtype):
+    """V magnitudes grow by 2^12 along each sequence (log-linear in the
+    position) and 2% of the rows are stored as zeros.  Each wave meets
+    larger v_scales step after step, so the power of two that keeps its
+    fp16 weights in range shrinks and the accumulator is rescaled many
+    times; the zero rows' weights underflow while their probabilities still
+    count.  Outputs stay O(1), so the usual gate applies."""
+    gen = torch.Generator().manual_seed(121)
+    lens = [5000, 777, 4096, 1, 300]
+    hq, hk = 32, 8
+    pages = sum((n + H.BLOCK - 1) // H.BLOCK for n in lens)
+    tables, slots = H.paged_layout(gen, lens, pages + 3)
+    n = slots.numel()
+    pos = torch.cat([torch.arange(x) for x in lens]).float()
+    grow = torch.exp2(12.0 * pos / max(lens) - 12.0)
+    key = H.randn(gen, (n, hk, H.D), dtype)
+    value = torch.randn(n, hk, H.D, generator=gen) * grow[:, None, None]
+    value[torch.rand(n, generator=gen) < 0.02] = 0.0
+    value = value.to(dtype)
+    query = H.randn(gen, (len(lens), hq, H.D), dtype)
+    caches = H.alloc_cache(pages + 3, H.BLOCK, hk)
+    store_fp8_kvcache(key.to(H.DEV), value.to(H.DEV), *caches, slots.to(H.DEV))
+    (max_abs, rel), _ = _run_and_check(query, lens, tables, caches)
+    print(f"growing V {dtype}: max_abs {max_abs:.3e} rel {rel:.3e}")
+
+
 def test_decode_long_context_qwen3_32b():
     """131072 tokens at 64 q / 8 kv heads: split-KV across the whole GPU plus
     the log-sum-exp combine."""

@@ -193,6 +193,35 @@ def test_varlen_prefill_v_scale_ratio_inside_a_tile(r, dtype):
     assert rel < (2.5e-3 if dtype == torch.bfloat16 else 5e-4), rel
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_varlen_prefill_v_scale_growing_along_the_keys(dtype):
+    """V magnitudes grow by 2^12 along each sequence's keys and 2% of the V
+    rows are zeros.  Every 128-key tile brings a larger v_scale, so each
+    wave's power-of-two weight scale shrinks tile after tile and its
+    accumulator is rescaled; the zero rows' weights underflow while their
+    probabilities still count.  Outputs stay O(1)."""
+    gen = torch.Generator().manual_seed(271)
+    hq, hk = 32, 8
+    lq = [96, 200, 1]
+    lk = [96 + 1500, 200, 1 + 700]
+    nb = sum((n + H.BLOCK - 1) // H.BLOCK for n in lk) + 2
+    tables, slots = H.paged_layout(gen, lk, nb)
+    n = slots.numel()
+    pos = torch.cat([torch.arange(x) for x in lk]).float()
+    grow = torch.exp2(12.0 * pos / max(lk) - 12.0)
+    key = torch.randn(n, hk, H.D, generator=gen)
+    value = torch.randn(n, hk, H.D, generator=gen) * grow[:, None, None]
+    value[torch.rand(n, generator=gen) < 0.02] = 0.0
+    query = torch.randn(sum(lq), hq, H.D, generator=gen)
+    key, value, query = key.to(dtype), value.to(dtype), query.to(dtype)
+    caches = H.alloc_cache(nb, H.BLOCK, hk)
+    store_fp8_kvcache(key.to(H.DEV), value.to(H.DEV), *caches, slots.to(H.DEV))
+    cu_q = torch.tensor([0] + list(np.cumsum(lq)), dtype=torch.int32)
+    cu_k = torch.tensor([0] + list(np.cumsum(lk)), dtype=torch.int32)
+    max_abs, rel = _varlen_check(query, tables, caches, cu_q, cu_k, lq)
+    print(f"growing V {dtype}: max_abs {max_abs:.4e} rel {rel:.4e}")
+
+
 def test_varlen_prefill_empty_sequences_and_oversized_max_seqlen():
     """Sequences with no new tokens (one with a cached prefix, one empty) in
     the batch, and max_seqlen_q far above the longest query: the extra
