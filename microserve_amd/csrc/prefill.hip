@@ -79,6 +79,7 @@ struct PrefillArgs {
   int64_t num_blocks;
   int prefix_len;
   int hq, hk, group, gc, qgroups, tpr, bs, w;
+  int gc_magic;  // ceil(256 / gc): n / gc == (n * gc_magic) >> 8 for n < 16
   float scale_log2;
 };
 
@@ -113,6 +114,8 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
   __shared__ __attribute__((aligned(16))) uint8_t v_lds1[kPStep * kHeadDim];
   __shared__ __attribute__((aligned(16))) float sc_lds0[2][kPStep];
   __shared__ __attribute__((aligned(16))) float sc_lds1[2][kPStep];
+  // each wave's fp16 v_scale * fw of the current tile's keys
+  __shared__ __attribute__((aligned(16))) _Float16 vsf_lds[kPWaves][kPStep];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -156,9 +159,10 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
   float qs[kPBlocks];
 #pragma unroll
   for (int b = 0; b < kPBlocks; ++b) {
-    const int qi = w_q0 + b * a.tpr + n / a.gc;
+    const int nq = (n * a.gc_magic) >> 8;  // n / gc
+    const int qi = w_q0 + b * a.tpr + nq;
     row_ok[b] = n < a.tpr * a.gc && qi < lq;
-    qh[b] = kvh * a.group + qgi * 16 + n % a.gc;
+    qh[b] = kvh * a.group + qgi * 16 + n - nq * a.gc;
     lim[b] = row_ok[b] ? prefix + qi + 1 : 0;
     // lane (g, n) holds d in [32g, 32g+32) of its row
     float x[32];
@@ -204,21 +208,23 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
     }
   }
 
-  f32x4 acc[kPBlocks][8];
-#pragma unroll
-  for (int b = 0; b < kPBlocks; ++b)
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) acc[b][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m[kPBlocks], l[kPBlocks];
+  // acc: O^T in units of fw, the power-of-two scale applied to v_scale (0
+  // until the first tile with a stored token sets it); lacc: the softmax
+  // denominator, as the output tile of an all-ones A operand against P^T,
+  // so every row of it holds its column's sum of the fp16 probabilities
+  f32x4 acc[kPBlocks][8], lacc[kPBlocks];
+  float m[kPBlocks];
 #pragma unroll
   for (int b = 0; b < kPBlocks; ++b) {
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) acc[b][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    lacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
     m[b] = -INFINITY;
-    l[b] = 0.0f;
   }
-  // acc and l are kept in units of fw, the power-of-two scale applied to
-  // p * v_scale (0 until the first tile with a stored token sets it);
-  // lf = log2(fw) is folded into the exp argument
-  float fw = 0.0f, lf = 0.0f;
+  float fw = 0.0f;
+  f16x8 ones;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) ones[i] = (_Float16)1.0f;
 
   // K operand: key n of each 16-key group, 16-byte chunks 2g and 2g + 1;
   // the swizzle of rows 16t + n does not depend on t
@@ -348,20 +354,19 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
         for (int b = 0; b < kPBlocks; ++b) {
           const float m_new = fmaxf(m[b], tm[b]);
           const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[b] - m_new);
-          l[b] *= alpha;
+          lacc[b] *= alpha;
 #pragma unroll
           for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= alpha;
           m[b] = m_new;
         }
       }
       // The PV product runs on v_mfma_f32_16x16x32_f16.  V converts to fp16
-      // exactly, and each weight is fp16(p * v_scale * fw), 11 significant
-      // bits.  fw is a power of two per wave, set from the largest v_scale
-      // the wave has seen: v_scale * fw <= kPVScaleMax, so with p <= 2^8
-      // (the lazy rescale's slack) no weight leaves fp16's range.  It only
-      // ever shrinks, and the accumulator and l are then rescaled by the
-      // exact ratio.  log2(fw) is folded into the exp argument, so exp2
-      // returns p * fw, which l sums in fp32.
+      // exactly, and each weight is fp16(p) * fp16(v_scale * fw), formed in
+      // pairs by v_pk_mul_f16.  fw is a power of two per wave, set from the
+      // largest v_scale the wave has seen: v_scale * fw <= kPVScaleMax, so
+      // with p <= 2^8 (the lazy rescale's slack) no weight leaves fp16's
+      // range.  It only ever shrinks, and the accumulator is then rescaled
+      // by the exact ratio; the output is divided by it at the end.
       {
         float vm = fmaxf(vss[lane], vss[64 + lane]);
         vm = max_xor32(max_xor16(max16_dpp(vm)));
@@ -370,47 +375,69 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
           if (fw != 0.0f) {
             const float r = fnew / fw;  // a power of two: exact
 #pragma unroll
-            for (int b = 0; b < kPBlocks; ++b) {
-              l[b] *= r;
+            for (int b = 0; b < kPBlocks; ++b)
 #pragma unroll
               for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= r;
-            }
           }
           fw = fnew;
-          lf = (float)((int)((__float_as_uint(fnew) >> 23) & 0xFFu) - 127);
         }
       }
+      // fp16(v_scale * fw) of the tile's keys, computed once per key by
+      // this wave (lane i: keys i and 64 + i) and read back in groups of
+      // four; the wave reads only its own writes, so a wave-level barrier
+      // orders them
+      _Float16* vsw = vsf_lds[wave];
+      vsw[lane] = (_Float16)(vss[lane] * fw);
+      vsw[64 + lane] = (_Float16)(vss[64 + lane] * fw);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       float m_use[kPBlocks];
 #pragma unroll
-      for (int b = 0; b < kPBlocks; ++b) m_use[b] = (m[b] == -INFINITY ? 0.0f : m[b]) - lf;
+      for (int b = 0; b < kPBlocks; ++b) m_use[b] = m[b] == -INFINITY ? 0.0f : m[b];
       // The wave raises its priority over the P loop and the PV MFMAs and
       // drops it after.
       __builtin_amdgcn_s_setprio(1);
       // P^T for the f16 MFMA: 32-key chunk c of the tile is S^T tiles 2c and
       // 2c + 1, so lane (g, n) holds keys 32c + 4g + r and 32c + 16 + 4g + r
       // of row n -- the order in which ds_read_b64_tr_b8 hands it V^T
-      // Each 16-key group's v_scales are read once for both blocks, one
-      // group ahead: read per block and group, every read's LDS latency was
-      // exposed.
+      // Each 16-key group's scales are read once for both blocks, one group
+      // ahead: read per block and group, every read's LDS latency was
+      // exposed.  The denominator's MFMA for a chunk follows its probabilities.
+      typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
       f16x8 pw[kPBlocks][4];
-      float psum[kPBlocks] = {};
-      f32x4 vsc_next = *reinterpret_cast<const f32x4*>(vss + 4 * g);
+      f16x4 vsf_next = *reinterpret_cast<const f16x4*>(vsw + 4 * g);
 #pragma unroll
-      for (int tt = 0; tt < 8; ++tt) {
-        const f32x4 vsc = vsc_next;
-        if (tt < 7) vsc_next = *reinterpret_cast<const f32x4*>(vss + 16 * (tt + 1) + 4 * g);
+      for (int c = 0; c < 4; ++c) {
+        f16x8 pc[kPBlocks];
 #pragma unroll
-        for (int b = 0; b < kPBlocks; ++b) {
+        for (int h = 0; h < 2; ++h) {
+          const int tt = 2 * c + h;
+          const f16x4 vf = vsf_next;
+          if (tt < 7) vsf_next = *reinterpret_cast<const f16x4*>(vsw + 16 * (tt + 1) + 4 * g);
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float pf = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b]));
-            psum[b] += pf;
-            pw[b][tt >> 1][4 * (tt & 1) + r] = (_Float16)(pf * vsc[r]);
+          for (int b = 0; b < kPBlocks; ++b) {
+            float pf[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) pf[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b]));
+            const f16x2 p01 = {(_Float16)pf[0], (_Float16)pf[1]};
+            const f16x2 p23 = {(_Float16)pf[2], (_Float16)pf[3]};
+            const f16x2 w01 = p01 * f16x2{vf[0], vf[1]};
+            const f16x2 w23 = p23 * f16x2{vf[2], vf[3]};
+            pc[b][4 * h + 0] = p01[0];
+            pc[b][4 * h + 1] = p01[1];
+            pc[b][4 * h + 2] = p23[0];
+            pc[b][4 * h + 3] = p23[1];
+            pw[b][c][4 * h + 0] = w01[0];
+            pw[b][c][4 * h + 1] = w01[1];
+            pw[b][c][4 * h + 2] = w23[0];
+            pw[b][c][4 * h + 3] = w23[1];
           }
         }
-      }
 #pragma unroll
-      for (int b = 0; b < kPBlocks; ++b) l[b] += psum[b];
+        for (int b = 0; b < kPBlocks; ++b)
+          lacc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pc[b], lacc[b], 0, 0, 0);
+      }
       // O^T += V^T . P^T, one 16-wide d tile and 32-key chunk per MFMA.  The
       // V^T reads of d tile dt + 1 are issued before the MFMAs of tile dt:
       // with one read in flight, each chunk's LDS latency sat behind only
@@ -464,12 +491,20 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
     }
   }
 
+  // The rows' coordinates are recomputed from the lane id rather than kept
+  // live across the loop, which would spill them.
+  int n_out = lane & 15;
+  asm volatile("" : "+v"(n_out));
 #pragma unroll
   for (int b = 0; b < kPBlocks; ++b) {
-    const float lt = sum_xor32(sum_xor16(l[b]));
-    if (!row_ok[b]) continue;
-    const float scale = lt > 0.0f ? 1.0f / lt : 0.0f;
-    uint16_t* op = a.out + ((int64_t)(q_begin + w_q0 + b * a.tpr + n / a.gc) * a.hq + qh[b]) * kHeadDim;
+    const float lt = lacc[b][0];
+    const int nq = (n_out * a.gc_magic) >> 8;  // n / gc
+    const int qi = w_q0 + b * a.tpr + nq;
+    if (!(n_out < a.tpr * a.gc && qi < lq)) continue;
+    // acc is in units of fw (a power of two): 1 / fw is exact
+    const float scale = lt > 0.0f && fw > 0.0f ? (1.0f / lt) * (1.0f / fw) : 0.0f;
+    const int qhb = kvh * a.group + qgi * 16 + n_out - nq * a.gc;
+    uint16_t* op = a.out + ((int64_t)(q_begin + qi) * a.hq + qhb) * kHeadDim;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) {
       const f32x4 o = acc[b][dt] * scale;
@@ -528,6 +563,7 @@ extern "C" int mskv_fp8_prefill_attention(
   a.gc = group < 16 ? group : 16;
   a.qgroups = group <= 16 ? 1 : group / 16;
   a.tpr = 16 / a.gc;
+  a.gc_magic = (256 + a.gc - 1) / a.gc;
   a.bs = block_size;
   a.w = max_blocks_per_seq;
   a.scale_log2 = softmax_scale * mskv::kLog2e;
