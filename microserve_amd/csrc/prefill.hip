@@ -28,10 +28,11 @@
 //    lane (g, n) holding 32 keys of row n, exactly the B-operand layout of
 //    P^T, so probabilities never move between lanes; V^T comes out of LDS
 //    with ds_read_b64_tr_b8 and converts to fp16 exactly.  Each weight is
-//    fp16(p * v_scale * fw), fw a per-wave power of two set from the largest
-//    v_scale seen, so the weights keep 11 significant bits whatever the
-//    spread of v_scale inside a tile.  The softmax denominator sums p * fw
-//    in fp32.
+//    fp16(p) * fp16(v_scale * fw) (v_pk_mul_f16), fw a per-wave power of
+//    two set from the largest v_scale seen, so the weights keep 11
+//    significant bits whatever the spread of v_scale inside a tile.  The
+//    softmax denominator is a ninth output tile: an all-ones A operand
+//    against the fp16 probabilities, summed in fp32 by the MFMA.
 //  * Online softmax in base 2 with a lazy rescale: the accumulator is
 //    rescaled only when some row's max grows by more than 2^8.  Masks are
 //    evaluated only on tiles that straddle the causal diagonal or the end
