@@ -107,12 +107,11 @@ struct StepLoads {
 };
 
 
-__device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
-                                          int t0, int t_end, int lane,
-                                          StepLoads& s) {
+// Issues the loads of the step at token t0, whose page holds block `blk`.
+__device__ __forceinline__ void load_step(const DecodeArgs& a, int blk, int kvh, int t0,
+                                          int t_end, int lane, StepLoads& s) {
   const int page = t0 / a.bs;
   const int off = t0 - page * a.bs;
-  const int blk = a.bt[(int64_t)b * a.w + page];
   const bool ok = blk >= 0 && (int64_t)blk < a.num_blocks;
   const int64_t bo = ok ? blk : 0;
   const uint32_t page_bytes = (uint32_t)a.bs * a.hk * kHeadDim;
@@ -138,10 +137,11 @@ __device__ __forceinline__ void load_step(const DecodeArgs& a, int b, int kvh,
 // sequence b for kv head kvh (q head qh of the lane's column): returns the
 // un-normalized accumulator O^T, the running max m (log2 units) and the
 // lane's share of the denominator l.  kv_lds / s_lds are this wave's own
-// double-buffered LDS tiles.
+// double-buffered LDS tiles; blk_first is the block of t_begin's page.
 template <typename T>
 __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int kvh, int qh,
-                                             bool head_ok, int t_begin, int t_end, int lane,
+                                             bool head_ok, int t_begin, int t_end,
+                                             int blk_first, int lane,
                                              uint8_t (&kv_lds)[2][2][kStep * kHeadDim],
                                              float (&s_lds)[2][2 * kStep], f32x4 (&acc)[8],
                                              float& m, float& l) {
@@ -223,14 +223,16 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int kvh
   const uint32_t k_lo = tile_off(n, g), k_hi = tile_off(n, 4 + g);
 
   StepLoads cur, nxt;
-  load_step(a, b, kvh, t_begin, t_end, lane, cur);
+  load_step(a, blk_first, kvh, t_begin, t_end, lane, cur);
   stage(cur, 0);
   wave_lds_sync();
   int buf = 0;
   for (int t0 = t_begin; t0 < t_end; t0 += kStep, buf ^= 1) {
     const int valid = cur.valid;
     const bool more = t0 + kStep < t_end;
-    if (more) load_step(a, b, kvh, t0 + kStep, t_end, lane, nxt);
+    if (more)
+      load_step(a, a.bt[(int64_t)b * a.w + (t0 + kStep) / a.bs], kvh, t0 + kStep, t_end, lane,
+                nxt);
 
     // S^T = K . Q^T for tokens [0,16) and [16,32) of the step
     const uint8_t* kt = kv_lds[buf][0];
@@ -362,15 +364,24 @@ void decode_fp8_kernel(DecodeArgs a) {
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, n = lane & 15;
   const int unit = blockIdx.x * W + wave, split = blockIdx.y, b = blockIdx.z;
+  // The sequence length and the split's first block id are read together,
+  // first thing, so the first K/V loads wait for one memory round trip, not
+  // a chain of them (readfirstlane is convergent, so the compiler cannot
+  // sink either read below the branches that use it).  The split's first
+  // page is inside the table: split * pages_per_split < w for every split
+  // count the host accepts.
+  const int len_raw = __builtin_amdgcn_readfirstlane(a.seqlens[b]);
+  const int blk_first =
+      __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b * a.w + split * a.pages_per_split]);
   if (unit >= a.hk * a.qgroups) return;
   const int kvh = unit / a.qgroups;
   const int hig = (unit - kvh * a.qgroups) * 16 + n;  // head within its group
   const bool head_ok = hig < a.group;
   const int qh = kvh * a.group + hig;
-  // tokens past the block table's width are not addressable: ignore them
-  const int L = min(a.seqlens[b], a.w * a.bs);
   const int split_tokens = a.pages_per_split * a.bs;
   const int t_begin = split * split_tokens;
+  // tokens past the block table's width are not addressable: ignore them
+  const int L = min(len_raw, a.w * a.bs);
 
   if (L <= 0) {
     if (a.splits == 1 && split == 0 && head_ok) {
@@ -386,7 +397,7 @@ void decode_fp8_kernel(DecodeArgs a) {
 
   f32x4 acc[8];
   float m, l;
-  attend_range<T>(a, b, kvh, qh, head_ok, t_begin, t_end, lane, kv_lds_all[wave],
+  attend_range<T>(a, b, kvh, qh, head_ok, t_begin, t_end, blk_first, lane, kv_lds_all[wave],
                   s_lds_all[wave], acc, m, l);
 
   // splits that hold tokens of this sequence; a sequence that fits in one
@@ -402,9 +413,108 @@ void decode_fp8_kernel(DecodeArgs a) {
   write_partial(a.part_o + row * kHeadDim, a.part_lse + row, acc, m, l, g);
 }
 
+// A merge state over some splits of one row, held in plain registers: the
+// largest lse value m, and den = sum 2^(lse_s - m), o = sum 2^(lse_s - m)
+// o_s over those splits, for four consecutive d.  m = -inf (den = 0, o = 0)
+// holds no split.
+//
+// Folds the splits sp = first + k * stride (k < K, sp < nvalid) of one row
+// into (m, den, o): every lse value and partial quad is loaded before any
+// is used, so the K splits cost one memory round trip.  Partials past
+// nvalid are never read.
+template <int K>
+__device__ __forceinline__ void merge_splits(float& m, float& den, f32x4& o,
+                                             const float* __restrict__ lse,
+                                             const float* __restrict__ po, int first,
+                                             int stride, int nvalid) {
+  float ls[K];
+  f32x4 pv[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int sp = first + k * stride;
+    const bool ok = sp < nvalid;
+    ls[k] = ok ? lse[sp] : -INFINITY;
+    pv[k] = ok ? *reinterpret_cast<const f32x4*>(po + (int64_t)sp * kHeadDim)
+               : f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  float cm = ls[0];
+#pragma unroll
+  for (int k = 1; k < K; ++k) cm = fmaxf(cm, ls[k]);
+  const float nm = fmaxf(m, cm);
+  if (nm == -INFINITY) return;  // no split here, none before
+  const float sc = m == -INFINITY ? 0.0f : exp2_fast(m - nm);
+  den *= sc;
+  o *= sc;
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const float w = exp2_fast(ls[k] - nm);  // 0 for a split not read
+    den += w;
+    o += w * pv[k];
+  }
+  m = nm;
+}
+
+// (m, den, o) becomes the merge of states a and b over disjoint splits.
+__device__ __forceinline__ void merge_pair(float& m, float& den, f32x4& o, float ma,
+                                           float da, f32x4 oa, float mb, float db, f32x4 ob) {
+  const float M = fmaxf(ma, mb);
+  if (M == -INFINITY) {
+    m = -INFINITY;
+    den = 0.0f;
+    o = f32x4{0.f, 0.f, 0.f, 0.f};
+    return;
+  }
+  const float sa = exp2_fast(ma - M), sb = exp2_fast(mb - M);  // 0 for -inf
+  m = M;
+  den = da * sa + db * sb;
+  o = oa * sa + ob * sb;
+}
+
+// Merges the state with that of lane l ^ 16 (v_permlane16_swap) or l ^ 32
+// (v_permlane32_swap), no LDS round trip: the swap returns both lanes'
+// values, in the same order for every field, so the pair's merge is the
+// same state on both lanes.
+template <bool kXor32>
+__device__ __forceinline__ uint2 swap_pair(float v) {
+  const auto r = kXor32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v),
+                                                           __float_as_uint(v), false, false)
+                        : __builtin_amdgcn_permlane16_swap(__float_as_uint(v),
+                                                           __float_as_uint(v), false, false);
+  return uint2{r[0], r[1]};
+}
+template <bool kXor32>
+__device__ __forceinline__ void merge_across(float& m, float& den, f32x4& o) {
+  const uint2 pm = swap_pair<kXor32>(m), pd = swap_pair<kXor32>(den);
+  const uint2 p0 = swap_pair<kXor32>(o[0]), p1 = swap_pair<kXor32>(o[1]);
+  const uint2 p2 = swap_pair<kXor32>(o[2]), p3 = swap_pair<kXor32>(o[3]);
+  merge_pair(m, den, o, __uint_as_float(pm.x), __uint_as_float(pd.x),
+             f32x4{__uint_as_float(p0.x), __uint_as_float(p1.x), __uint_as_float(p2.x),
+                   __uint_as_float(p3.x)},
+             __uint_as_float(pm.y), __uint_as_float(pd.y),
+             f32x4{__uint_as_float(p0.y), __uint_as_float(p1.y), __uint_as_float(p2.y),
+                   __uint_as_float(p3.y)});
+}
+
+// out = o / den in the activation type, four consecutive d (zeros when
+// den == 0)
+template <typename T>
+__device__ __forceinline__ void write_merged(uint16_t* op, float den, f32x4 o) {
+  using A = Act<T>;
+  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
+  o *= inv;
+  const uint32_t lo = (uint32_t)A::from_f32(o[0]) | ((uint32_t)A::from_f32(o[1]) << 16);
+  const uint32_t hi = (uint32_t)A::from_f32(o[2]) | ((uint32_t)A::from_f32(o[3]) << 16);
+  *reinterpret_cast<u32x2*>(op) = u32x2{lo, hi};
+}
+
 // out[b, h, :] = sum_s 2^(lse_s - M) o_s / sum_s 2^(lse_s - M) over the
 // splits holding tokens of sequence b; zeros for an empty sequence.  Rows
 // whose sequence fits in one split were written by the split kernel.
+// One wave per (b, h) row: lane (j, i) takes d in [4i, 4i + 4) of splits
+// j, j + 2, ..., kLoopK of them per memory round trip (32 splits: the
+// ragged batch's whole row in one), and the two halves merge across lanes.
+constexpr int kLoopK = 16;
+
 template <typename T>
 __global__ __launch_bounds__(64) void decode_combine_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
@@ -413,38 +523,27 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(
   const int row = blockIdx.x;  // b * hq + h
   const int b = row / hq;
   const int lane = threadIdx.x;
+  const int j = lane >> 5, i = lane & 31;
   const int L = min(seqlens[b], max_tokens);
   const int nvalid = L <= 0 ? 0 : min(splits, (L + split_tokens - 1) / split_tokens);
   if (nvalid == 1) return;
   const float* lse = part_lse + (int64_t)row * splits;
-  float M = -INFINITY;
-#pragma unroll 8
-  for (int s = 0; s < nvalid; ++s) M = fmaxf(M, lse[s]);
-  float o0 = 0.0f, o1 = 0.0f, den = 0.0f;
-  if (M != -INFINITY) {
-    const float* po = part_o + (int64_t)row * splits * kHeadDim + 2 * lane;
-#pragma unroll 8
-    for (int s = 0; s < nvalid; ++s) {
-      const float w = exp2_fast(lse[s] - M);
-      const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)s * kHeadDim);
-      o0 += w * v.x;
-      o1 += w * v.y;
-      den += w;
-    }
-  }
-  const float inv = den > 0.0f ? 1.0f / den : 0.0f;
-  const uint32_t pk = (uint32_t)Act<T>::from_f32(o0 * inv) |
-                      ((uint32_t)Act<T>::from_f32(o1 * inv) << 16);
-  *reinterpret_cast<uint32_t*>(out + (int64_t)row * kHeadDim + 2 * lane) = pk;
+  const float* po = part_o + (int64_t)row * splits * kHeadDim + 4 * i;
+  float m = -INFINITY, den = 0.0f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int base = 0; base < nvalid; base += 2 * kLoopK)
+    merge_splits<kLoopK>(m, den, o, lse, po, base + j, 2, nvalid);
+  merge_across<true>(m, den, o);
+  if (j == 0) write_merged<T>(out + (int64_t)row * kHeadDim + 4 * i, den, o);
 }
 
 // The same merge for at most S splits (S a compile-time bound, small): every
 // split's lse value and partial row is loaded at once, before the sequence
-// length arrives, so a row costs one memory round trip instead of three.
+// length arrives, so a row costs one memory round trip instead of two.
 // Rows of few splits use them all; with many splits, mostly unused (ragged
-// batches), the reads of unused rows cost more than the round trips, so
-// those keep decode_combine_kernel.  The arithmetic is
-// decode_combine_kernel's, operation for operation.
+// batches), the reads of unused rows cost more than the round trip, so
+// those keep decode_combine_kernel.  M is the largest valid lse value and
+// the weighted sum runs in split order.
 template <typename T, int S>
 __global__ __launch_bounds__(64) void decode_combine_small_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
@@ -489,11 +588,14 @@ __global__ __launch_bounds__(64) void decode_combine_small_kernel(
   *reinterpret_cast<uint32_t*>(out + (int64_t)row * kHeadDim + 2 * lane) = pk;
 }
 
-// The same merge for many splits (long contexts): one 1024-thread workgroup
-// per (b, h) row.  Every thread reads lse values for the maximum; wave w then
-// accumulates splits w, w + 16, ... (eight partial rows in flight per lane)
-// and the sixteen waves' sums are merged through LDS.
-constexpr int kWideWaves = 16;
+// The same merge for many splits (long contexts): four 256-thread
+// workgroups per (b, h) row, each taking 32 d of it, so a batch-1 decode's
+// 64 rows fill the chip.  Lane (j, i) of wave w takes d 4i..4i+3 of the
+// quarter and splits 8w + j, 8w + j + 32, ..., kWideK of them per memory
+// round trip (256 splits in one); the 32 lanes of each d merge across
+// lanes (xor 8, 16, 32), then the four waves through LDS.
+constexpr int kWideWaves = 4;
+constexpr int kWideK = 8;
 constexpr int kWideThreshold = 64;  // splits above this use the wide merge
 
 template <typename T>
@@ -501,56 +603,43 @@ __global__ __launch_bounds__(64 * kWideWaves) void decode_combine_wide_kernel(
     const float* __restrict__ part_o, const float* __restrict__ part_lse,
     const int32_t* __restrict__ seqlens, uint16_t* __restrict__ out, int hq, int splits,
     int split_tokens, int max_tokens) {
-  __shared__ float s_max[kWideWaves];
-  __shared__ float s_den[kWideWaves];
-  __shared__ __attribute__((aligned(16))) float s_o[kWideWaves][kHeadDim];
+  __shared__ float s_m[kWideWaves][8], s_den[kWideWaves][8];
+  __shared__ __attribute__((aligned(16))) f32x4 s_o[kWideWaves][8];
   const int row = blockIdx.x;  // b * hq + h
+  const int quarter = blockIdx.y;
   const int b = row / hq;
   const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wave = tid >> 6;
   const int lane = tid & 63;
+  const int i = lane & 7, j = lane >> 3;
   const int L = min(seqlens[b], max_tokens);
   const int nvalid = L <= 0 ? 0 : min(splits, (L + split_tokens - 1) / split_tokens);
   if (nvalid == 1) return;  // written by the split kernel
+  const int d = 32 * quarter + 4 * i;
   const float* lse = part_lse + (int64_t)row * splits;
-  float mx = -INFINITY;
-  for (int sp = tid; sp < nvalid; sp += 64 * kWideWaves) mx = fmaxf(mx, lse[sp]);
-#pragma unroll
-  for (int mask = 1; mask < 16; mask <<= 1) mx = wave_max_xor(mx, mask);
-  mx = max_xor32(max_xor16(mx));
-  if (lane == 0) s_max[wave] = mx;
-  __syncthreads();
-  float M = s_max[0];
-#pragma unroll
-  for (int w = 1; w < kWideWaves; ++w) M = fmaxf(M, s_max[w]);
-  float o0 = 0.0f, o1 = 0.0f, den = 0.0f;
-  if (M != -INFINITY) {
-    const float* po = part_o + (int64_t)row * splits * kHeadDim + 2 * lane;
-#pragma unroll 8
-    for (int sp = wave; sp < nvalid; sp += kWideWaves) {
-      const float w = exp2_fast(lse[sp] - M);
-      const float2 v = *reinterpret_cast<const float2*>(po + (int64_t)sp * kHeadDim);
-      o0 += w * v.x;
-      o1 += w * v.y;
-      den += w;
-    }
+  const float* po = part_o + (int64_t)row * splits * kHeadDim + d;
+  float m = -INFINITY, den = 0.0f;
+  f32x4 o = {0.f, 0.f, 0.f, 0.f};
+  for (int base = 0; base < nvalid; base += 8 * kWideWaves * kWideK)
+    merge_splits<kWideK>(m, den, o, lse, po, base + 8 * wave + j, 8 * kWideWaves, nvalid);
+  {
+    const f32x4 ox = {__shfl_xor(o[0], 8), __shfl_xor(o[1], 8), __shfl_xor(o[2], 8),
+                      __shfl_xor(o[3], 8)};
+    merge_pair(m, den, o, m, den, o, __shfl_xor(m, 8), __shfl_xor(den, 8), ox);
   }
-  s_o[wave][2 * lane] = o0;
-  s_o[wave][2 * lane + 1] = o1;
-  if (lane == 0) s_den[wave] = den;
-  __syncthreads();
-  if (wave != 0) return;
-  float a0 = 0.0f, a1 = 0.0f, d = 0.0f;
-#pragma unroll
-  for (int w = 0; w < kWideWaves; ++w) {
-    a0 += s_o[w][2 * lane];
-    a1 += s_o[w][2 * lane + 1];
-    d += s_den[w];
+  merge_across<false>(m, den, o);
+  merge_across<true>(m, den, o);
+  if (j == 0) {
+    s_m[wave][i] = m;
+    s_den[wave][i] = den;
+    s_o[wave][i] = o;
   }
-  const float inv = d > 0.0f ? 1.0f / d : 0.0f;
-  const uint32_t pk = (uint32_t)Act<T>::from_f32(a0 * inv) |
-                      ((uint32_t)Act<T>::from_f32(a1 * inv) << 16);
-  *reinterpret_cast<uint32_t*>(out + (int64_t)row * kHeadDim + 2 * lane) = pk;
+  __syncthreads();
+  if (wave != 0 || j != 0) return;
+#pragma unroll
+  for (int w = 1; w < kWideWaves; ++w)
+    merge_pair(m, den, o, m, den, o, s_m[w][i], s_den[w][i], s_o[w][i]);
+  write_merged<T>(out + (int64_t)row * kHeadDim + d, den, o);
 }
 
 static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
@@ -579,7 +668,7 @@ static hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stre
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || a.splits == 1) return e;
   if (a.splits > kWideThreshold)
-    hipLaunchKernelGGL(decode_combine_wide_kernel<T>, dim3((unsigned)(batch * a.hq)),
+    hipLaunchKernelGGL(decode_combine_wide_kernel<T>, dim3((unsigned)(batch * a.hq), 4u),
                        dim3(64 * kWideWaves), 0, stream, a.part_o, a.part_lse, a.seqlens, a.out,
                        a.hq, a.splits, a.pages_per_split * a.bs, a.w * a.bs);
   else if (a.splits <= 8)
