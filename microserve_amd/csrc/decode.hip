@@ -47,7 +47,9 @@
 //    heads of a token range, whole 1 KiB token rows, 132 KB of LDS: one per
 //    CU) while the grid holds at most 512 of them, about two rounds; 4
 //    waves (half a token row each, two per CU) for larger grids, whose
-//    smaller last round halves the tail.
+//    smaller last round halves the tail.  Those grids of many rounds run
+//    their sequences longest-first: a pre-pass ranks them by length on the
+//    device, so short sequences fill the last round.
 //  * Every page is read through a buffer resource sized to that page; an
 //    invalid block id gives a zero-length resource (loads return 0) and its
 //    tokens are masked, so a bad table entry cannot fault.
@@ -95,7 +97,12 @@ struct DecodeArgs {
   uint16_t* out;
   float* part_o;
   float* part_lse;
-  int hq, hk, group, qgroups, bs, w, splits, pages_per_split;
+  // Longest-first order (grids of many rounds, else null): entry z of the
+  // batch's entries is (sequence, length) of the z-th longest sequence;
+  // right after them, int32 [batch, splits]: the block id of each split's
+  // first page of that sequence.
+  const int2* order;
+  int batch, hq, hk, group, qgroups, bs, w, splits, pages_per_split;
   int64_t num_blocks;
   float scale_log2;
 };
@@ -363,16 +370,30 @@ void decode_fp8_kernel(DecodeArgs a) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, n = lane & 15;
-  const int unit = blockIdx.x * W + wave, split = blockIdx.y, b = blockIdx.z;
-  // The sequence length and the split's first block id are read together,
-  // first thing, so the first K/V loads wait for one memory round trip, not
-  // a chain of them (readfirstlane is convergent, so the compiler cannot
-  // sink either read below the branches that use it).  The split's first
+  const int unit = blockIdx.x * W + wave, split = blockIdx.y;
+  // The sequence, its length and the split's first block id are read
+  // together, first thing, so the first K/V loads wait for one memory round
+  // trip, not a chain of them (readfirstlane is convergent, so the compiler
+  // cannot sink a read below the branches that use it).  The split's first
   // page is inside the table: split * pages_per_split < w for every split
-  // count the host accepts.
-  const int len_raw = __builtin_amdgcn_readfirstlane(a.seqlens[b]);
-  const int blk_first =
-      __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b * a.w + split * a.pages_per_split]);
+  // count the host accepts.  With an order, grid row z takes the z-th
+  // longest sequence, so long sequences start first and short ones fill
+  // the last round.
+  int b, len_raw, blk_first;
+  if (a.order) {
+    const int32_t* first_blk = reinterpret_cast<const int32_t*>(a.order + a.batch);
+    const int2 e = a.order[blockIdx.z];
+    b = __builtin_amdgcn_readfirstlane(e.x);
+    len_raw = __builtin_amdgcn_readfirstlane(e.y);
+    blk_first =
+        __builtin_amdgcn_readfirstlane(first_blk[(int64_t)blockIdx.z * a.splits + split]);
+    if ((unsigned)b >= (unsigned)a.batch) return;  // the pre-pass writes a permutation
+  } else {
+    b = blockIdx.z;
+    len_raw = __builtin_amdgcn_readfirstlane(a.seqlens[b]);
+    blk_first =
+        __builtin_amdgcn_readfirstlane(a.bt[(int64_t)b * a.w + split * a.pages_per_split]);
+  }
   if (unit >= a.hk * a.qgroups) return;
   const int kvh = unit / a.qgroups;
   const int hig = (unit - kvh * a.qgroups) * 16 + n;  // head within its group
@@ -642,7 +663,76 @@ __global__ __launch_bounds__(64 * kWideWaves) void decode_combine_wide_kernel(
   write_merged<T>(out + (int64_t)row * kHeadDim + d, den, o);
 }
 
+// The longest-first order of the sequences, for split grids of many
+// rounds: workgroup b ranks sequence b by its length (clamped to the
+// table; ties by index, so the ranks are a permutation) and writes its
+// entry and every split's first block id at that rank.  The block ids are
+// read alongside the lengths, so the rank costs one memory round trip
+// before the writes.
+constexpr int kOrderThreads = 256;
+constexpr int kOrderMaxBatch = 4096;
+
+// Sum over the wave with DPP row shifts and the two cross-row swaps (no
+// LDS round trip).
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);  // row_mirror
+  const auto r16 = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  v = (int)(r16[0] + r16[1]);
+  const auto r32 = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)(r32[0] + r32[1]);
+}
+
+__global__ __launch_bounds__(kOrderThreads) void decode_order_kernel(
+    const int32_t* __restrict__ seqlens, const int32_t* __restrict__ bt, int2* __restrict__ order,
+    int32_t* __restrict__ first_blk, int batch, int w, int max_tokens, int splits,
+    int pages_per_split) {
+  __shared__ int s_cnt[kOrderThreads / 64];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int len_b = seqlens[b];
+  // this thread's first split's block id, read with the lengths
+  const int blk0 = tid < splits ? bt[(int64_t)b * w + tid * pages_per_split] : 0;
+  const int key = max(0, min(len_b, max_tokens));
+  int cnt = 0;
+  for (int j = tid; j < batch; j += kOrderThreads) {
+    const int kj = max(0, min(seqlens[j], max_tokens));
+    cnt += (kj > key || (kj == key && j < b)) ? 1 : 0;
+  }
+  cnt = wave_sum_i32(cnt);
+  if ((tid & 63) == 0) s_cnt[tid >> 6] = cnt;
+  __syncthreads();
+  int rank = 0;
+#pragma unroll
+  for (int i = 0; i < kOrderThreads / 64; ++i) rank += s_cnt[i];
+  if (tid == 0) order[rank] = int2{b, len_b};
+  if (tid < splits) first_blk[(int64_t)rank * splits + tid] = blk0;
+  for (int sp = tid + kOrderThreads; sp < splits; sp += kOrderThreads)
+    first_blk[(int64_t)rank * splits + sp] = bt[(int64_t)b * w + sp * pages_per_split];
+}
+
 static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
+
+// Whether a decode shape runs its sequences longest-first: split grids of
+// many rounds (the 4-wave shape), where a long sequence dispatched late
+// sets the makespan (ragged batch 256: 436 against 452 us with the rows
+// presorted).  Shapes only, like every launch choice here.
+constexpr int64_t kOrderMaxEntries = 1 << 16;  // batch * splits
+static bool ordered_of(int batch, int hk, int qgroups, int splits) {
+  const int64_t wide_wgs =
+      (int64_t)((hk * qgroups + kWavesPerWG - 1) / kWavesPerWG) * splits * batch;
+  return splits > 1 && batch > 1 && batch <= kOrderMaxBatch && wide_wgs > kWideGridMax &&
+         (int64_t)batch * splits <= kOrderMaxEntries;
+}
+
+// Bytes of the split partials ([batch, hq, splits, 128] outputs, then
+// [batch, hq, splits] lse values), rounded up to 256.
+static size_t partials_bytes(int batch, int hq, int splits) {
+  const size_t raw = (size_t)batch * hq * splits * (kHeadDim + 1) * sizeof(float);
+  return (raw + 255) & ~(size_t)255;
+}
 
 template <typename T>
 static hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream) {
@@ -654,6 +744,14 @@ static hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stre
   // is the same on every call of a captured graph.
   const int units = a.hk * a.qgroups;
   const int64_t wide_wgs = (int64_t)((units + kWavesPerWG - 1) / kWavesPerWG) * a.splits * batch;
+  if (a.order) {
+    int2* order = const_cast<int2*>(a.order);
+    hipLaunchKernelGGL(decode_order_kernel, dim3((unsigned)batch), dim3(kOrderThreads), 0, stream,
+                       a.seqlens, a.bt, order, reinterpret_cast<int32_t*>(order + batch), batch,
+                       a.w, a.w * a.bs, a.splits, a.pages_per_split);
+    const hipError_t eo = hipGetLastError();
+    if (eo != hipSuccess) return eo;
+  }
   if (wide_wgs <= kWideGridMax) {
     const dim3 grid((unsigned)((units + kWavesPerWG - 1) / kWavesPerWG), (unsigned)a.splits,
                     (unsigned)batch);
@@ -711,7 +809,13 @@ extern "C" size_t mskv_decode_workspace_bytes(int batch, int num_q_heads,
   if (num_splits <= 1 || batch <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
       head_dim <= 0 || num_q_heads % num_kv_heads != 0)
     return 0;
-  return (size_t)batch * num_q_heads * num_splits * (head_dim + 1) * sizeof(float);
+  size_t bytes = (size_t)batch * num_q_heads * num_splits * (head_dim + 1) * sizeof(float);
+  const int qgroups = mskv::qgroups_of(num_q_heads / num_kv_heads);
+  if (head_dim == mskv::kHeadDim &&
+      mskv::ordered_of(batch, num_kv_heads, qgroups, num_splits))
+    bytes = mskv::partials_bytes(batch, num_q_heads, num_splits) + (size_t)batch * sizeof(int2) +
+            (size_t)batch * num_splits * sizeof(int32_t);
+  return bytes;
 }
 
 namespace mskv {
@@ -759,6 +863,11 @@ static int decode_checked(const void* query, const void* k_cache, const void* v_
   a.part_o = need > 0 ? (float*)workspace : nullptr;
   a.part_lse = need > 0 ? a.part_o + (size_t)batch * num_q_heads * num_splits * head_dim
                         : nullptr;
+  a.order = nullptr;
+  if (need > 0 && ordered_of(batch, num_kv_heads, qgroups_of(group), num_splits))
+    a.order = (const int2*)((uint8_t*)workspace +
+                            partials_bytes(batch, num_q_heads, num_splits));
+  a.batch = batch;
   a.hq = num_q_heads;
   a.hk = num_kv_heads;
   a.group = group;

@@ -162,8 +162,9 @@ def test_decode_ragged_fragmented(dtype):
     """Ragged lengths, log-uniform in [16, 32768], blocks sampled from a
     fragmented pool.  17 splits x 48 sequences is 816 eight-wave workgroups,
     over the launcher's limit for that shape, so this runs the 4-wave
-    workgroup shape (the Qwen3-8B full shape, 256 workgroups, runs the
-    8-wave one), in both activation types."""
+    workgroup shape with its longest-first pre-pass (the Qwen3-8B full
+    shape, 256 workgroups, runs the 8-wave one in row order), in both
+    activation types."""
     gen = torch.Generator().manual_seed(101)
     b = 48
     lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(32768), generator=gen)).long().tolist()
@@ -294,6 +295,57 @@ def test_decode_graph_replay_matches_eager():
             else:
                 same = torch.equal(a[: nb - 1], b_[: nb - 1])
             assert same, f"cache differs after replay {it}"
+
+
+def test_decode_graph_replay_longest_first_order():
+    """The longest-first pre-pass (shapes of many workgroup rounds) inside a
+    captured graph: each replay ranks the sequences by their new lengths,
+    ties and empty rows included, and equals the eager result bit for bit;
+    the first replay is also checked against the oracle."""
+    hq, hk, b = 32, 8, 48
+    gen = torch.Generator().manual_seed(171)
+    lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(16384), generator=gen)).long().tolist()
+    lens[0] = 16384                      # the table is 64 pages wide: 16 splits
+    pages = [(n + H.BLOCK - 1) // H.BLOCK for n in lens]
+    query, tables, caches = _setup(172, lens, hq, hk, sum(pages) + 7)
+    width = tables.shape[1]
+    assert b * decode_num_splits(b, hq, hk, width, H.BLOCK) > 512
+    scale = H.D ** -0.5
+    q_d = query.to(H.DEV)
+    tables_d = tables.to(H.DEV)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=H.DEV)
+    out = torch.zeros_like(q_d)
+
+    def step():
+        fp8_decode_attention(q_d, *caches, lens_d, tables_d, scale, out=out)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for it in range(3):
+        # new lengths inside each row's pages: a new ranking every replay,
+        # with repeated lengths and empty rows
+        new = [int(torch.randint(0, p * H.BLOCK + 1, (1,), generator=gen)) for p in pages]
+        new[1] = new[2] = new[3]
+        new[4] = 0
+        lens_d.copy_(torch.tensor(new, dtype=torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = out.clone()
+        want = fp8_decode_attention(q_d, *caches, lens_d, tables_d, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), f"replay {it}"
+        assert (got[4] == 0).all()
+        if it == 0:
+            kc, vc, ks, vs = H.cache_to_numpy(*caches)
+            ref = O.decode_attention(query, kc, vc, ks, vs, torch.tensor(new, dtype=torch.int32),
+                                     tables, scale)
+            H.assert_attention_close(got, ref, 2e-2, 1e-2)
 
 
 def test_decode_scratch_reuse_across_shapes():
