@@ -73,7 +73,7 @@ int mskv_decode_num_splits(int batch, int num_q_heads, int num_kv_heads,
 /*
  * Scratch bytes mskv_fp8_decode_attention needs for num_splits (0 if 1):
  * the fp32 split partials and, for shapes of many workgroup rounds, the
- * longest-first order of the sequences that a pre-pass kernel writes.
+ * longest-first work items that a pre-pass kernel writes.
  * Contents on entry do not matter.
  */
 size_t mskv_decode_workspace_bytes(int batch, int num_q_heads,

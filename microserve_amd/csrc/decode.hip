@@ -48,8 +48,9 @@
 //    CU) while the grid holds at most 512 of them, about two rounds; 4
 //    waves (half a token row each, two per CU) for larger grids, whose
 //    smaller last round halves the tail.  Those grids of many rounds run
-//    their sequences longest-first: a pre-pass ranks them by length on the
-//    device, so short sequences fill the last round.
+//    compacted work items longest-first: a pre-pass ranks the sequences by
+//    length on the device and lists their valid splits, so short sequences
+//    fill the last round and empty splits exit at the end of the grid.
 //  * Every page is read through a buffer resource sized to that page; an
 //    invalid block id gives a zero-length resource (loads return 0) and its
 //    tokens are masked, so a bad table entry cannot fault.
@@ -97,11 +98,11 @@ struct DecodeArgs {
   uint16_t* out;
   float* part_o;
   float* part_lse;
-  // Longest-first order (grids of many rounds, else null): entry z of the
-  // batch's entries is (sequence, length) of the z-th longest sequence;
-  // right after them, int32 [batch, splits]: the block id of each split's
-  // first page of that sequence.
-  const int2* order;
+  // Work items longest-first (grids of many rounds, else null): item i is
+  // (sequence, split, length, block id of the split's first page), for
+  // the valid splits of the sequences in order of decreasing length; the
+  // item count is stored just before item 0.
+  const int4* items;
   int batch, hq, hk, group, qgroups, bs, w, splits, pages_per_split;
   int64_t num_blocks;
   float scale_log2;
@@ -370,25 +371,29 @@ void decode_fp8_kernel(DecodeArgs a) {
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int g = lane >> 4, n = lane & 15;
-  const int unit = blockIdx.x * W + wave, split = blockIdx.y;
+  const int unit = blockIdx.x * W + wave;
   // The sequence, its length and the split's first block id are read
   // together, first thing, so the first K/V loads wait for one memory round
   // trip, not a chain of them (readfirstlane is convergent, so the compiler
   // cannot sink a read below the branches that use it).  The split's first
   // page is inside the table: split * pages_per_split < w for every split
-  // count the host accepts.  With an order, grid row z takes the z-th
-  // longest sequence, so long sequences start first and short ones fill
-  // the last round.
-  int b, len_raw, blk_first;
-  if (a.order) {
-    const int32_t* first_blk = reinterpret_cast<const int32_t*>(a.order + a.batch);
-    const int2 e = a.order[blockIdx.z];
+  // count the host accepts.  With work items, grid row (z, y) takes item
+  // z * splits + y: the valid splits of the longest sequences first, short
+  // sequences' in the last round, and the rows past the last item (empty
+  // splits) at the end of the grid.
+  int b, split, len_raw, blk_first;
+  if (a.items) {
+    const int item = blockIdx.z * a.splits + blockIdx.y;
+    const int4 e = a.items[item];
+    const int count = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int*>(a.items)[-4]);
     b = __builtin_amdgcn_readfirstlane(e.x);
-    len_raw = __builtin_amdgcn_readfirstlane(e.y);
-    blk_first =
-        __builtin_amdgcn_readfirstlane(first_blk[(int64_t)blockIdx.z * a.splits + split]);
-    if ((unsigned)b >= (unsigned)a.batch) return;  // the pre-pass writes a permutation
+    split = __builtin_amdgcn_readfirstlane(e.y);
+    len_raw = __builtin_amdgcn_readfirstlane(e.z);
+    blk_first = __builtin_amdgcn_readfirstlane(e.w);
+    if (item >= count) return;
+    if ((unsigned)b >= (unsigned)a.batch || (unsigned)split >= (unsigned)a.splits) return;
   } else {
+    split = blockIdx.y;
     b = blockIdx.z;
     len_raw = __builtin_amdgcn_readfirstlane(a.seqlens[b]);
     blk_first =
@@ -663,12 +668,13 @@ __global__ __launch_bounds__(64 * kWideWaves) void decode_combine_wide_kernel(
   write_merged<T>(out + (int64_t)row * kHeadDim + d, den, o);
 }
 
-// The longest-first order of the sequences, for split grids of many
-// rounds: workgroup b ranks sequence b by its length (clamped to the
-// table; ties by index, so the ranks are a permutation) and writes its
-// entry and every split's first block id at that rank.  The block ids are
-// read alongside the lengths, so the rank costs one memory round trip
-// before the writes.
+// The longest-first work items of a split grid of many rounds: workgroup
+// b ranks sequence b by its length (clamped to the table; ties by index,
+// so the order is total) and sums the valid splits of the sequences ahead
+// of it, which is where its items start; it writes one item per valid
+// split of its own.  Workgroup 0 also writes the item count.  The block
+// ids are read alongside the lengths, so the items cost one memory round
+// trip before the writes.
 constexpr int kOrderThreads = 256;
 constexpr int kOrderMaxBatch = 4096;
 
@@ -686,39 +692,49 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
 }
 
 __global__ __launch_bounds__(kOrderThreads) void decode_order_kernel(
-    const int32_t* __restrict__ seqlens, const int32_t* __restrict__ bt, int2* __restrict__ order,
-    int32_t* __restrict__ first_blk, int batch, int w, int max_tokens, int splits,
-    int pages_per_split) {
-  __shared__ int s_cnt[kOrderThreads / 64];
+    const int32_t* __restrict__ seqlens, const int32_t* __restrict__ bt, int4* __restrict__ items,
+    int batch, int w, int max_tokens, int splits, int pages_per_split, int split_tokens) {
+  __shared__ int s_off[kOrderThreads / 64], s_tot[kOrderThreads / 64];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
   const int len_b = seqlens[b];
   // this thread's first split's block id, read with the lengths
   const int blk0 = tid < splits ? bt[(int64_t)b * w + tid * pages_per_split] : 0;
   const int key = max(0, min(len_b, max_tokens));
-  int cnt = 0;
+  const int nv_b = min(splits, (key + split_tokens - 1) / split_tokens);
+  int off = 0, tot = 0;
   for (int j = tid; j < batch; j += kOrderThreads) {
     const int kj = max(0, min(seqlens[j], max_tokens));
-    cnt += (kj > key || (kj == key && j < b)) ? 1 : 0;
+    const int nj = min(splits, (kj + split_tokens - 1) / split_tokens);
+    off += (kj > key || (kj == key && j < b)) ? nj : 0;
+    tot += nj;
   }
-  cnt = wave_sum_i32(cnt);
-  if ((tid & 63) == 0) s_cnt[tid >> 6] = cnt;
+  off = wave_sum_i32(off);
+  tot = wave_sum_i32(tot);
+  if ((tid & 63) == 0) {
+    s_off[tid >> 6] = off;
+    s_tot[tid >> 6] = tot;
+  }
   __syncthreads();
-  int rank = 0;
+  int first = 0, count = 0;
 #pragma unroll
-  for (int i = 0; i < kOrderThreads / 64; ++i) rank += s_cnt[i];
-  if (tid == 0) order[rank] = int2{b, len_b};
-  if (tid < splits) first_blk[(int64_t)rank * splits + tid] = blk0;
-  for (int sp = tid + kOrderThreads; sp < splits; sp += kOrderThreads)
-    first_blk[(int64_t)rank * splits + sp] = bt[(int64_t)b * w + sp * pages_per_split];
+  for (int i = 0; i < kOrderThreads / 64; ++i) {
+    first += s_off[i];
+    count += s_tot[i];
+  }
+  if (b == 0 && tid == 0) reinterpret_cast<int*>(items)[-4] = count;
+  if (tid < nv_b) items[first + tid] = int4{b, tid, len_b, blk0};
+  for (int sp = tid + kOrderThreads; sp < nv_b; sp += kOrderThreads)
+    items[first + sp] = int4{b, sp, len_b, bt[(int64_t)b * w + sp * pages_per_split]};
 }
 
 static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
 
-// Whether a decode shape runs its sequences longest-first: split grids of
-// many rounds (the 4-wave shape), where a long sequence dispatched late
-// sets the makespan (ragged batch 256: 436 against 452 us with the rows
-// presorted).  Shapes only, like every launch choice here.
+// Whether a decode shape runs compacted work items longest-first: split
+// grids of many rounds (the 4-wave shape), where a long sequence
+// dispatched late sets the makespan and most workgroups are empty splits
+// (ragged batch 256: 433 against 454 us).  Shapes only, like every launch
+// choice here.
 constexpr int64_t kOrderMaxEntries = 1 << 16;  // batch * splits
 static bool ordered_of(int batch, int hk, int qgroups, int splits) {
   const int64_t wide_wgs =
@@ -744,11 +760,10 @@ static hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stre
   // is the same on every call of a captured graph.
   const int units = a.hk * a.qgroups;
   const int64_t wide_wgs = (int64_t)((units + kWavesPerWG - 1) / kWavesPerWG) * a.splits * batch;
-  if (a.order) {
-    int2* order = const_cast<int2*>(a.order);
+  if (a.items) {
     hipLaunchKernelGGL(decode_order_kernel, dim3((unsigned)batch), dim3(kOrderThreads), 0, stream,
-                       a.seqlens, a.bt, order, reinterpret_cast<int32_t*>(order + batch), batch,
-                       a.w, a.w * a.bs, a.splits, a.pages_per_split);
+                       a.seqlens, a.bt, const_cast<int4*>(a.items), batch, a.w, a.w * a.bs,
+                       a.splits, a.pages_per_split, a.pages_per_split * a.bs);
     const hipError_t eo = hipGetLastError();
     if (eo != hipSuccess) return eo;
   }
@@ -813,8 +828,8 @@ extern "C" size_t mskv_decode_workspace_bytes(int batch, int num_q_heads,
   const int qgroups = mskv::qgroups_of(num_q_heads / num_kv_heads);
   if (head_dim == mskv::kHeadDim &&
       mskv::ordered_of(batch, num_kv_heads, qgroups, num_splits))
-    bytes = mskv::partials_bytes(batch, num_q_heads, num_splits) + (size_t)batch * sizeof(int2) +
-            (size_t)batch * num_splits * sizeof(int32_t);
+    bytes = mskv::partials_bytes(batch, num_q_heads, num_splits) + sizeof(int4) +
+            (size_t)batch * num_splits * sizeof(int4);
   return bytes;
 }
 
@@ -863,10 +878,10 @@ static int decode_checked(const void* query, const void* k_cache, const void* v_
   a.part_o = need > 0 ? (float*)workspace : nullptr;
   a.part_lse = need > 0 ? a.part_o + (size_t)batch * num_q_heads * num_splits * head_dim
                         : nullptr;
-  a.order = nullptr;
+  a.items = nullptr;
   if (need > 0 && ordered_of(batch, num_kv_heads, qgroups_of(group), num_splits))
-    a.order = (const int2*)((uint8_t*)workspace +
-                            partials_bytes(batch, num_q_heads, num_splits));
+    a.items = (const int4*)((uint8_t*)workspace +
+                            partials_bytes(batch, num_q_heads, num_splits) + sizeof(int4));
   a.batch = batch;
   a.hq = num_q_heads;
   a.hk = num_kv_heads;

@@ -52,10 +52,10 @@ def test_split_policy_depends_on_shapes_only():
     assert lib.mskv_decode_num_splits(4096, 32, 8, 4, 256) == 1
     assert lib.mskv_decode_workspace_bytes(64, 32, 8, 128, 1) == 0
     assert lib.mskv_decode_workspace_bytes(64, 32, 8, 128, 8) == 64 * 32 * 8 * 129 * 4
-    # 256 x 31 splits runs its sequences longest-first: the partials (padded
-    # to 256 bytes), then 8 bytes per sequence and 4 per (sequence, split)
+    # 256 x 31 splits runs longest-first work items: the partials (padded to
+    # 256 bytes), a 16-byte item count, then 16 bytes per (sequence, split)
     part = (256 * 32 * 31 * 129 * 4 + 255) // 256 * 256
-    assert lib.mskv_decode_workspace_bytes(256, 32, 8, 128, 31) == part + 256 * 8 + 256 * 31 * 4
+    assert lib.mskv_decode_workspace_bytes(256, 32, 8, 128, 31) == part + 16 + 256 * 31 * 16
 
 
 def test_argument_validation_without_launch():
