@@ -43,14 +43,15 @@
 //    agent-scope fences, i.e. an L2 writeback + invalidate per XCD, which
 //    measured 2x slower).  A sequence that fits in one split is written
 //    directly by the split kernel.
+//  * Grids of many rounds (over 512 eight-wave workgroups) run compacted
+//    work items longest-first: a pre-pass ranks the sequences by length on
+//    the device and lists their valid splits, so short sequences fill the
+//    last round and empty splits exit at the end of the grid.
 //  * Two workgroup shapes, chosen from shapes alone: 8 waves (all 8 kv
 //    heads of a token range, whole 1 KiB token rows, 132 KB of LDS: one per
-//    CU) while the grid holds at most 512 of them, about two rounds; 4
-//    waves (half a token row each, two per CU) for larger grids, whose
-//    smaller last round halves the tail.  Those grids of many rounds run
-//    compacted work items longest-first: a pre-pass ranks the sequences by
-//    length on the device and lists their valid splits, so short sequences
-//    fill the last round and empty splits exit at the end of the grid.
+//    CU), and 4 waves (half a token row each, two per CU) for grids of many
+//    rounds without work items (past the items' limits, or fewer than 8
+//    units per kv head group), whose smaller last round halves the tail.
 //  * Every page is read through a buffer resource sized to that page; an
 //    invalid block id gives a zero-length resource (loads return 0) and its
 //    tokens are masked, so a bad table entry cannot fault.
@@ -754,10 +755,12 @@ template <typename T>
 static hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stream) {
   // One 8-wave workgroup (128 KB of LDS) fills a CU.  A grid of at most
   // kWideGridMax of those runs in about two rounds; a larger grid runs in
-  // many, and the last round's tail halves with 4-wave workgroups (two per
-  // CU): ragged batch 256, 452 against 491 us; the Qwen3-8B batch 64 x 4096
-  // step prefers 8 waves, 88.3 against 90.5 us.  Shapes only, so the choice
-  // is the same on every call of a captured graph.
+  // many, over the longest-first work items of the pre-pass.  Beyond the
+  // items' limits (and where a kv head group has fewer than eight units),
+  // the last round's tail halves with 4-wave workgroups (two per CU):
+  // ragged batch 256 in row order, 452 against 491 us.  The Qwen3-8B batch
+  // 64 x 4096 step prefers 8 waves, 88.3 against 90.5 us.  Shapes only, so
+  // the choice is the same on every call of a captured graph.
   const int units = a.hk * a.qgroups;
   const int64_t wide_wgs = (int64_t)((units + kWavesPerWG - 1) / kWavesPerWG) * a.splits * batch;
   if (a.items) {
@@ -767,7 +770,10 @@ static hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stre
     const hipError_t eo = hipGetLastError();
     if (eo != hipSuccess) return eo;
   }
-  if (wide_wgs <= kWideGridMax) {
+  // 8-wave workgroups also run the work items when every wave has a unit:
+  // with the short sequences last, their longer units no longer lengthen
+  // the tail (ragged batch 256: 425-426 against 433-435 us with 4 waves)
+  if (wide_wgs <= kWideGridMax || (a.items && units >= kWavesPerWG)) {
     const dim3 grid((unsigned)((units + kWavesPerWG - 1) / kWavesPerWG), (unsigned)a.splits,
                     (unsigned)batch);
     hipLaunchKernelGGL((decode_fp8_kernel<T, kWavesPerWG>), grid, dim3(64 * kWavesPerWG), 0,

@@ -161,10 +161,9 @@ def test_decode_block_relabel_and_split_invariance():
 def test_decode_ragged_fragmented(dtype):
     """Ragged lengths, log-uniform in [16, 32768], blocks sampled from a
     fragmented pool.  17 splits x 48 sequences is 816 eight-wave workgroups,
-    over the launcher's limit for that shape, so this runs the 4-wave
-    workgroup shape with its longest-first pre-pass (the Qwen3-8B full
-    shape, 256 workgroups, runs the 8-wave one in row order), in both
-    activation types."""
+    over the launcher's limit for row order, so this runs the longest-first
+    work items of the pre-pass (the Qwen3-8B full shape, 256 workgroups,
+    runs in row order), in both activation types."""
     gen = torch.Generator().manual_seed(101)
     b = 48
     lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(32768), generator=gen)).long().tolist()
@@ -174,9 +173,10 @@ def test_decode_ragged_fragmented(dtype):
 
 
 def test_decode_narrow_workgroups_wide_gqa_group():
-    """GQA 32 (64 q / 2 kv heads: two 16-head units per kv head) on the
-    4-wave workgroup shape: 96 sequences x 16 splits of one 8-wave
-    workgroup each is over the launcher's limit."""
+    """GQA 32 (64 q / 2 kv heads: two 16-head units per kv head, four in
+    all) on the 4-wave workgroup shape over the work items: 96 sequences x
+    16 splits of one 8-wave workgroup each is over the launcher's limit for
+    row order, and eight waves would leave four idle."""
     gen = torch.Generator().manual_seed(105)
     b = 96
     lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(16384), generator=gen)).long().tolist()
@@ -185,6 +185,24 @@ def test_decode_narrow_workgroups_wide_gqa_group():
     pages = sum((n + 255) // 256 for n in lens)
     query, tables, caches = _setup(106, lens, 64, 2, pages + 5, torch.float16)
     _run_and_check(query, lens, tables, caches)
+
+
+def test_decode_row_order_past_the_work_item_limit():
+    """300 sequences x 256 splits (32-token pages, 1024 pages wide) is past
+    the work items' limit of 65,536 (sequence, split) pairs: this runs the
+    4-wave workgroups in row order, empty splits interleaved."""
+    gen = torch.Generator().manual_seed(181)
+    b, bs = 300, 32
+    lens = torch.exp(torch.empty(b).uniform_(np.log(1), np.log(2048), generator=gen)).long().tolist()
+    lens[7] = 1024 * bs                  # the table is 1024 pages wide
+    lens[8] = 0
+    splits = decode_num_splits(b, 8, 8, 1024, bs)
+    assert b * splits > 65536
+    pages = sum((n + bs - 1) // bs for n in lens)
+    query, tables, caches = _setup(182, lens, 8, 8, pages + 3, block_size=bs)
+    assert tables.shape[1] == 1024
+    _, out = _run_and_check(query, lens, tables, caches)
+    assert (out[8] == 0).all()
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
