@@ -27,10 +27,14 @@
 //   Store: the bytes and scales of store_fp8_kvcache on the rotated k and on
 //   v (microserve/layers/fp8_kv_cache.py:11-39).
 //
-// Work layout: eight lanes own one (token, row) pair, row = one of the
-// num_q_heads + 2 * num_kv_heads heads of the token; lane l holds elements
-// [8l, 8l+8) and [64+8l, 64+8l+8), so rotate_half's pairs (d, d+64) meet in
-// one lane and the only cross-lane traffic is the two DPP reductions.
+// Work layout: eight lanes own a chunk of up to four rows of one kind (q, k
+// or v heads) of one token; lane l holds elements [8l, 8l+8) and
+// [64+8l, 64+8l+8) of each, so rotate_half's pairs (d, d+64) meet in one
+// lane and the only cross-lane traffic is the two DPP reductions.  The
+// token's rotary rows and the norm weights are unpacked once per chunk, not
+// once per row (the kernel is bound by VALU issue, not by HBM).  The grid
+// lists every token's q chunks, then the k chunks, then the v chunks, so a
+// wave's groups take the same path.
 #include <math.h>
 
 #include "fp8_row.h"
@@ -40,8 +44,8 @@
 namespace mskv {
 
 constexpr int kNrThreads = 256;
-constexpr int kNrRowsPerBlock = kNrThreads / 8;  // rows in flight per pass
-constexpr int kNrRowsPerGroup = 2;
+constexpr int kNrGroups = kNrThreads / 8;  // 8-lane groups per workgroup
+constexpr int kNrChunk = 4;                // rows per group: heads of one kind, one token
 
 struct NormRopeArgs {
   const uint16_t* q;
@@ -63,6 +67,8 @@ struct NormRopeArgs {
   int64_t rows, num_slots, max_position;
   int hq, hk, heads;
   float eps;
+  int cq, ck;               // chunks per token of q heads, of k (and v) heads
+  int64_t q_chunks, k_chunks, chunks;  // over all tokens: q, k (= v), all
 };
 
 // Sum over the 8 lanes of a row group: xor 1, xor 2, then the mirrored
@@ -113,60 +119,40 @@ __device__ __forceinline__ u32x4 pack8(const float* x) {
   return r;
 }
 
-// One row: x holds its 16 elements (lane layout above), already loaded.
+// RMSNorm (when w is given) and rotary of one q or k row in place: x holds
+// its 16 elements (lane layout above); wv, c, s are the lane's norm weights
+// and its token's cos/sin values; a row whose position is out of range
+// becomes zeros.
 template <typename T>
-__device__ __forceinline__ void finish_row(const NormRopeArgs& a, int64_t tok, int j, int64_t pos,
-                                           int64_t slot, int sub, float* x) {
+__device__ __forceinline__ void norm_rope_row(const NormRopeArgs& a, bool has_w, bool pos_ok,
+                                              const float* wv, const float* c, const float* s,
+                                              float* x) {
 #pragma clang fp contract(off)
-  const bool pos_ok = pos >= 0 && pos < a.max_position;
-  const int lo = 8 * sub, hi = kHeadDim / 2 + 8 * sub;
-  const bool is_v = j >= a.hq + a.hk;
-  if (!is_v) {
-    const uint16_t* w = j < a.hq ? a.q_weight : a.k_weight;
-    if (w) {
-      float ss = 0.0f;
+  if (has_w) {
+    float ss = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) ss += x[i] * x[i];  // each square is exact
-      const float var = sum8_dpp(ss) / (float)kHeadDim;
-      const float r = 1.0f / sqrtf(var + a.eps);
-      float wv[16];
-      unpack8<T>(*reinterpret_cast<const u32x4*>(w + lo), wv);
-      unpack8<T>(*reinterpret_cast<const u32x4*>(w + hi), wv + 8);
+    for (int i = 0; i < 16; ++i) ss += x[i] * x[i];  // each square is exact
+    const float var = sum8_dpp(ss) / (float)kHeadDim;
+    const float r = 1.0f / sqrtf(var + a.eps);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = rnd<T>(rnd_f32<T>(x[i] * r) * wv[i]);
-    }
-    float c[16], s[16];
-    const int64_t tab = (pos_ok ? pos : 0) * kHeadDim;
-    unpack8<T>(*reinterpret_cast<const u32x4*>(a.cos + tab + lo), c);
-    unpack8<T>(*reinterpret_cast<const u32x4*>(a.cos + tab + hi), c + 8);
-    unpack8<T>(*reinterpret_cast<const u32x4*>(a.sin + tab + lo), s);
-    unpack8<T>(*reinterpret_cast<const u32x4*>(a.sin + tab + hi), s + 8);
-    float o[16];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      o[i] = rnd<T>(rnd<T>(x[i] * c[i]) + (-rnd<T>(x[8 + i] * s[i])));
-      o[8 + i] = rnd<T>(rnd<T>(x[8 + i] * c[8 + i]) + rnd<T>(x[i] * s[8 + i]));
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = pos_ok ? o[i] : 0.0f;
-    uint16_t* dst = nullptr;
-    if (j < a.hq)
-      dst = a.q_out + (tok * a.hq + j) * kHeadDim;
-    else if (a.k_out)
-      dst = a.k_out + (tok * a.hk + (j - a.hq)) * kHeadDim;
-    if (dst) {
-      __builtin_nontemporal_store(pack8<T>(x), reinterpret_cast<u32x4*>(dst + lo));
-      __builtin_nontemporal_store(pack8<T>(x + 8), reinterpret_cast<u32x4*>(dst + hi));
-    }
-    if (j < a.hq) return;
+    for (int i = 0; i < 16; ++i) x[i] = rnd<T>(rnd_f32<T>(x[i] * r) * wv[i]);
   }
+  float o[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    o[i] = rnd<T>(rnd<T>(x[i] * c[i]) + (-rnd<T>(x[8 + i] * s[i])));
+    o[8 + i] = rnd<T>(rnd<T>(x[8 + i] * c[8 + i]) + rnd<T>(x[i] * s[8 + i]));
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] = pos_ok ? o[i] : 0.0f;
+}
 
-  // k (rotated) or v: FP8 row and its scale
+// The FP8 row and scale of a k (rotated) or v row, at cache row `dst`.
+__device__ __forceinline__ void store_fp8_row(const NormRopeArgs& a, bool is_v, int64_t dst,
+                                              int sub, const float* x) {
+  const int lo = 8 * sub, hi = kHeadDim / 2 + 8 * sub;
   u32x4 qb;
   const float scale = quantize16(x, qb);
-  if (!pos_ok || slot < 0 || slot >= a.num_slots) return;
-  const int head = is_v ? j - a.hq - a.hk : j - a.hq;
-  const int64_t dst = slot * a.hk + head;
   uint8_t* cache = is_v ? a.v_cache : a.k_cache;
   __builtin_nontemporal_store(u32x2{qb[0], qb[1]},
                               reinterpret_cast<u32x2*>(cache + dst * kHeadDim + lo));
@@ -175,53 +161,90 @@ __device__ __forceinline__ void finish_row(const NormRopeArgs& a, int64_t tok, i
   if (sub == 0) (is_v ? a.v_scale : a.k_scale)[dst] = scale;
 }
 
-// Each 8-lane group owns kNrRowsPerGroup rows, kNrRowsPerBlock apart, and
-// issues the loads of all of them before finishing the first: twice the
-// bytes in flight per lane at the same occupancy.
+// Each 8-lane group owns one chunk: up to kNrChunk consecutive heads of one
+// kind of one token.  It issues the loads of all its rows first, then
+// unpacks the token's rotary values and the norm weights once for them.
 template <typename T, typename SlotT>
 __global__ __launch_bounds__(kNrThreads) void qk_norm_rope_store_kernel(NormRopeArgs a) {
   const int sub = threadIdx.x & 7;
-  const int64_t first = (int64_t)blockIdx.x * (kNrRowsPerBlock * kNrRowsPerGroup) +
-                        (threadIdx.x >> 3);
+  const int64_t chunk = (int64_t)blockIdx.x * kNrGroups + (threadIdx.x >> 3);
+  if (chunk >= a.chunks) return;  // whole 8-lane groups leave together
   const int lo = 8 * sub, hi = kHeadDim / 2 + 8 * sub;
-  int64_t tok[kNrRowsPerGroup], pos[kNrRowsPerGroup], slot[kNrRowsPerGroup];
-  int jj[kNrRowsPerGroup];
-  u32x4 xl[kNrRowsPerGroup], xh[kNrRowsPerGroup];
-#pragma unroll
-  for (int u = 0; u < kNrRowsPerGroup; ++u) {
-    const int64_t row = first + (int64_t)u * kNrRowsPerBlock;
-    if (row >= a.rows) break;  // whole 8-lane groups leave together
-    // rows < 2^31 (checked on the host): 32-bit division
-    const uint32_t t32 = (uint32_t)row / (uint32_t)a.heads;
-    tok[u] = t32;
-    const int j = (int)((uint32_t)row - t32 * (uint32_t)a.heads);
-    jj[u] = j;
-    const uint16_t* src;
-    if (j < a.hq)
-      src = a.q + tok[u] * a.q_stride + (int64_t)j * kHeadDim;
-    else if (j < a.hq + a.hk)
-      src = a.k + tok[u] * a.k_stride + (int64_t)(j - a.hq) * kHeadDim;
-    else
-      src = a.v + tok[u] * a.v_stride + (int64_t)(j - a.hq - a.hk) * kHeadDim;
-    xl[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + lo));
-    xh[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + hi));
-    pos[u] = a.positions[tok[u]];
-    slot[u] = j < a.hq ? 0 : (int64_t)static_cast<const SlotT*>(a.slots)[tok[u]];
+  // kind 0: q heads, 1: k heads, 2: v heads; chunks < 2^31 (rows are,
+  // checked on the host): 32-bit division
+  int kind, per;
+  uint32_t c32;
+  if (chunk < a.q_chunks) {
+    kind = 0, per = a.cq, c32 = (uint32_t)chunk;
+  } else if (chunk < a.q_chunks + a.k_chunks) {
+    kind = 1, per = a.ck, c32 = (uint32_t)(chunk - a.q_chunks);
+  } else {
+    kind = 2, per = a.ck, c32 = (uint32_t)(chunk - a.q_chunks - a.k_chunks);
   }
+  const uint32_t t32 = c32 / (uint32_t)per;
+  const int64_t tok = t32;
+  const int h0 = (int)(c32 - t32 * (uint32_t)per) * kNrChunk;
+  const int nheads = kind == 0 ? a.hq : a.hk;
+  const int n = min(kNrChunk, nheads - h0);
+  const uint16_t* src = kind == 0   ? a.q + tok * a.q_stride
+                        : kind == 1 ? a.k + tok * a.k_stride
+                                    : a.v + tok * a.v_stride;
+  src += (int64_t)h0 * kHeadDim;
+  u32x4 xl[kNrChunk], xh[kNrChunk];
 #pragma unroll
-  for (int u = 0; u < kNrRowsPerGroup; ++u) {
-    if (first + (int64_t)u * kNrRowsPerBlock >= a.rows) return;
-    float x[16];
-    unpack8<T>(xl[u], x);
-    unpack8<T>(xh[u], x + 8);
-    finish_row<T>(a, tok[u], jj[u], pos[u], slot[u], sub, x);
+  for (int r = 0; r < kNrChunk; ++r) {
+    if (r < n) {
+      xl[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + r * kHeadDim + lo));
+      xh[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(src + r * kHeadDim + hi));
+    }
+  }
+  const int64_t pos = a.positions[tok];
+  const int64_t slot = kind == 0 ? 0 : (int64_t) static_cast<const SlotT*>(a.slots)[tok];
+  const bool pos_ok = pos >= 0 && pos < a.max_position;
+  // the cache takes k and v rows only at valid positions and slots
+  const bool to_cache = kind != 0 && pos_ok && slot >= 0 && slot < a.num_slots;
+  float x[16];
+  if (kind != 2) {
+    const uint16_t* w = kind == 0 ? a.q_weight : a.k_weight;
+    const bool has_w = w != nullptr;
+    float wv[16], c[16], s[16];
+    if (has_w) {
+      unpack8<T>(*reinterpret_cast<const u32x4*>(w + lo), wv);
+      unpack8<T>(*reinterpret_cast<const u32x4*>(w + hi), wv + 8);
+    }
+    const int64_t tab = (pos_ok ? pos : 0) * kHeadDim;
+    unpack8<T>(*reinterpret_cast<const u32x4*>(a.cos + tab + lo), c);
+    unpack8<T>(*reinterpret_cast<const u32x4*>(a.cos + tab + hi), c + 8);
+    unpack8<T>(*reinterpret_cast<const u32x4*>(a.sin + tab + lo), s);
+    unpack8<T>(*reinterpret_cast<const u32x4*>(a.sin + tab + hi), s + 8);
+#pragma unroll
+    for (int r = 0; r < kNrChunk; ++r) {
+      if (r >= n) break;
+      unpack8<T>(xl[r], x);
+      unpack8<T>(xh[r], x + 8);
+      norm_rope_row<T>(a, has_w, pos_ok, wv, c, s, x);
+      uint16_t* dst = kind == 0 ? a.q_out + (tok * a.hq + h0 + r) * kHeadDim
+                                : (a.k_out ? a.k_out + (tok * a.hk + h0 + r) * kHeadDim : nullptr);
+      if (dst) {
+        __builtin_nontemporal_store(pack8<T>(x), reinterpret_cast<u32x4*>(dst + lo));
+        __builtin_nontemporal_store(pack8<T>(x + 8), reinterpret_cast<u32x4*>(dst + hi));
+      }
+      if (to_cache) store_fp8_row(a, false, slot * a.hk + h0 + r, sub, x);
+    }
+  } else if (to_cache) {
+#pragma unroll
+    for (int r = 0; r < kNrChunk; ++r) {
+      if (r >= n) break;
+      unpack8<T>(xl[r], x);
+      unpack8<T>(xh[r], x + 8);
+      store_fp8_row(a, true, slot * a.hk + h0 + r, sub, x);
+    }
   }
 }
 
 template <typename T>
 static hipError_t launch_norm_rope(const NormRopeArgs& a, int slot_dtype, hipStream_t stream) {
-  const int64_t per_block = (int64_t)kNrRowsPerBlock * kNrRowsPerGroup;
-  const int64_t blocks = (a.rows + per_block - 1) / per_block;
+  const int64_t blocks = (a.chunks + kNrGroups - 1) / kNrGroups;
   if (slot_dtype == MSKV_INT64)
     hipLaunchKernelGGL((qk_norm_rope_store_kernel<T, int64_t>), dim3((unsigned)blocks),
                        dim3(kNrThreads), 0, stream, a);
@@ -274,6 +297,11 @@ extern "C" int mskv_qk_norm_rope_store(
                        (uint16_t*)q_out, (uint16_t*)k_out, (uint8_t*)k_cache,
                        (uint8_t*)v_cache, k_scale_cache, v_scale_cache, slot_mapping, rows,
                        num_slots, max_position, num_q_heads, num_kv_heads, heads, eps};
+  a.cq = (num_q_heads + mskv::kNrChunk - 1) / mskv::kNrChunk;
+  a.ck = (num_kv_heads + mskv::kNrChunk - 1) / mskv::kNrChunk;
+  a.q_chunks = num_tokens * a.cq;
+  a.k_chunks = num_tokens * a.ck;
+  a.chunks = a.q_chunks + 2 * a.k_chunks;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const hipError_t e = act_dtype == MSKV_BFLOAT16 ? mskv::launch_norm_rope<__bf16>(a, slot_dtype, s)
                                                    : mskv::launch_norm_rope<_Float16>(a, slot_dtype, s);
