@@ -283,7 +283,8 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
     }
     // the denominator: sums of the probabilities as rounded for the MFMA,
     // so each output is an exact convex combination of V rows under them
-    // (a chain of v_dot2 per pair did the same at 4% of the kernel's time)
+    // (a chain of v_dot2 per pair summed the same rounded values at 4% of
+    // the kernel's time)
     {
       x8 ones;
 #pragma unroll
