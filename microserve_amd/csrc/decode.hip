@@ -101,9 +101,10 @@ struct DecodeArgs {
   float* part_lse;
   // Work items longest-first (grids of many rounds, else null): item i is
   // (sequence, split, length, block id of the split's first page), for
-  // the valid splits of the sequences in order of decreasing length; the
-  // item count is stored just before item 0.
+  // the valid splits of the sequences in order of decreasing length, and
+  // item_count of them are valid.
   const int4* items;
+  const int* item_count;
   int batch, hq, hk, group, qgroups, bs, w, splits, pages_per_split;
   int64_t num_blocks;
   float scale_log2;
@@ -386,7 +387,7 @@ void decode_fp8_kernel(DecodeArgs a) {
   if (a.items) {
     const int item = blockIdx.z * a.splits + blockIdx.y;
     const int4 e = a.items[item];
-    const int count = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int*>(a.items)[-4]);
+    const int count = __builtin_amdgcn_readfirstlane(*a.item_count);
     b = __builtin_amdgcn_readfirstlane(e.x);
     split = __builtin_amdgcn_readfirstlane(e.y);
     len_raw = __builtin_amdgcn_readfirstlane(e.z);
@@ -694,7 +695,8 @@ __device__ __forceinline__ int wave_sum_i32(int v) {
 
 __global__ __launch_bounds__(kOrderThreads) void decode_order_kernel(
     const int32_t* __restrict__ seqlens, const int32_t* __restrict__ bt, int4* __restrict__ items,
-    int batch, int w, int max_tokens, int splits, int pages_per_split, int split_tokens) {
+    int* __restrict__ item_count, int batch, int w, int max_tokens, int splits,
+    int pages_per_split, int split_tokens) {
   __shared__ int s_off[kOrderThreads / 64], s_tot[kOrderThreads / 64];
   const int b = blockIdx.x;
   const int tid = threadIdx.x;
@@ -723,7 +725,7 @@ __global__ __launch_bounds__(kOrderThreads) void decode_order_kernel(
     first += s_off[i];
     count += s_tot[i];
   }
-  if (b == 0 && tid == 0) reinterpret_cast<int*>(items)[-4] = count;
+  if (b == 0 && tid == 0) *item_count = count;
   if (tid < nv_b) items[first + tid] = int4{b, tid, len_b, blk0};
   for (int sp = tid + kOrderThreads; sp < nv_b; sp += kOrderThreads)
     items[first + sp] = int4{b, sp, len_b, bt[(int64_t)b * w + sp * pages_per_split]};
@@ -765,8 +767,9 @@ static hipError_t launch_decode(const DecodeArgs& a, int batch, hipStream_t stre
   const int64_t wide_wgs = (int64_t)((units + kWavesPerWG - 1) / kWavesPerWG) * a.splits * batch;
   if (a.items) {
     hipLaunchKernelGGL(decode_order_kernel, dim3((unsigned)batch), dim3(kOrderThreads), 0, stream,
-                       a.seqlens, a.bt, const_cast<int4*>(a.items), batch, a.w, a.w * a.bs,
-                       a.splits, a.pages_per_split, a.pages_per_split * a.bs);
+                       a.seqlens, a.bt, const_cast<int4*>(a.items),
+                       const_cast<int*>(a.item_count), batch, a.w, a.w * a.bs, a.splits,
+                       a.pages_per_split, a.pages_per_split * a.bs);
     const hipError_t eo = hipGetLastError();
     if (eo != hipSuccess) return eo;
   }
@@ -884,10 +887,15 @@ static int decode_checked(const void* query, const void* k_cache, const void* v_
   a.part_o = need > 0 ? (float*)workspace : nullptr;
   a.part_lse = need > 0 ? a.part_o + (size_t)batch * num_q_heads * num_splits * head_dim
                         : nullptr;
+  // the work items follow the partials: a 16-byte slot for the count, then
+  // one 16-byte item per (sequence, split)
   a.items = nullptr;
-  if (need > 0 && ordered_of(batch, num_kv_heads, qgroups_of(group), num_splits))
-    a.items = (const int4*)((uint8_t*)workspace +
-                            partials_bytes(batch, num_q_heads, num_splits) + sizeof(int4));
+  a.item_count = nullptr;
+  if (need > 0 && ordered_of(batch, num_kv_heads, qgroups_of(group), num_splits)) {
+    uint8_t* base = (uint8_t*)workspace + partials_bytes(batch, num_q_heads, num_splits);
+    a.item_count = (const int*)base;
+    a.items = (const int4*)(base + sizeof(int4));
+  }
   a.batch = batch;
   a.hq = num_q_heads;
   a.hk = num_kv_heads;

@@ -2,8 +2,11 @@
 that allocates nothing (its split partials live in a library-owned device
 array): called through the C ABI, its output equals mskv_fp8_decode_attention's
 bit for bit on two calls in a row, the second with a smaller input (the array
-then holds the first call's partials), and a shape whose partials exceed
-the array is rejected."""
+then holds the first call's partials), then on a ragged batch whose grid runs
+the longest-first work items (kept in the same array); a shape whose
+partials exceed the array is rejected."""
+
+import numpy as np
 
 import ctypes
 
@@ -64,6 +67,32 @@ def test_noalloc_decode_equals_workspace_decode_twice():
     torch.cuda.synchronize()
     assert torch.equal(out2, want2)
     assert (out2[2] == 0).all()
+
+
+def test_noalloc_decode_work_items_in_the_array():
+    """48 ragged sequences x 17 splits: over 512 eight-wave workgroups, so the
+    pre-pass writes its work items after the partials in the array (14 MB in
+    all); two calls, the second with new lengths."""
+    scale = H.D ** -0.5
+    gen = torch.Generator().manual_seed(303)
+    b = 48
+    lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(32768), generator=gen)).long().tolist()
+    lens[0] = 32768
+    pages = sum((n + H.BLOCK - 1) // H.BLOCK for n in lens)
+    q, caches, seqlens, tables = _setup(304, lens, 32, 8, pages + 9)
+    lib = _lib.load()
+    splits = decode_num_splits(b, 32, 8, tables.shape[1], H.BLOCK)
+    assert b * splits > 512
+    assert lib.mskv_decode_workspace_bytes(b, 32, 8, H.D, splits) <= SCRATCH_BYTES
+    out = torch.empty_like(q)
+    for it in range(2):
+        if it:
+            seqlens = torch.tensor([max(0, n - 3 * n // 4) for n in lens], dtype=torch.int32,
+                                   device=H.DEV)
+        assert _noalloc(q, caches, seqlens, tables, out, scale) == 0
+        want = fp8_decode_attention(q, *caches, seqlens, tables, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"call {it}"
 
 
 def test_noalloc_decode_rejects_partials_over_the_limit():
