@@ -110,14 +110,15 @@ int mskv_fp8_decode_attention(const void* query, const void* k_cache,
                               int act_dtype, int num_splits, void* workspace,
                               size_t workspace_bytes, void* stream);
 
-/* Split-partials scratch the allocation-free decode holds per GPU. */
+/* Scratch (split partials, work items) the allocation-free decode holds per GPU. */
 #define MSKV_DECODE_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 
 /*
  * mskv_fp8_decode_attention without a workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, serving
  * loops and harnesses that forbid hipMalloc).  It has no counterpart in the
- * reference.  The split partials go to a library-owned device array of
+ * reference.  The split partials (and, for batches of many workgroup
+ * rounds, the pre-pass's work items) go to a library-owned device array of
  * MSKV_DECODE_NOALLOC_SCRATCH_BYTES (32 MiB) on each GPU, held until the
  * process ends; shapes whose mskv_decode_workspace_bytes exceeds it are
  * rejected with MSKV_EWORKSPACE (e.g. batch 64 x 4096 tokens at 32 q heads
