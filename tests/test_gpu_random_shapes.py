@@ -11,8 +11,8 @@ import torch
 
 from oracle import fp8_oracle as O
 from tests import gpu_helpers as H
-from microserve_amd import (fp8_decode_attention, fp8_varlen_prefill_attention,
-                            store_fp8_kvcache)
+from microserve_amd import (decode_num_splits, fp8_decode_attention,
+                            fp8_varlen_prefill_attention, store_fp8_kvcache)
 
 pytestmark = pytest.mark.gpu
 
@@ -50,6 +50,36 @@ def test_decode_random_shapes(case):
     kc, vc, ks, vs = H.cache_to_numpy(*caches)
     ref = O.decode_attention(query, kc, vc, ks, vs, seqlens, tables, scale)
     H.assert_attention_close(out, ref)
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_decode_random_shapes_work_items(case):
+    """Grids of over 512 eight-wave workgroups, so the pre-pass ranks the
+    sequences and lists their splits as work items (8-wave workgroups, or
+    4-wave ones when a kv head group has fewer than eight units): random
+    batches with zero, one-token, short and long contexts, ties included."""
+    rng = random.Random(5000 + case)
+    hq, hk = HEADS[case % len(HEADS)]
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    batch = rng.randint(40, 120)
+    lens = [rng.choice([0, 1, 700, rng.randint(1, 3000)]) for _ in range(batch)]
+    lens[rng.randrange(batch)] = rng.randint(16384, 24576)
+    gen = torch.Generator().manual_seed(6000 + case)
+    tables, caches = _fill(gen, lens, hk, H.BLOCK, dtype)
+    units = hk * (1 if hq // hk <= 16 else hq // hk // 16)
+    splits = decode_num_splits(batch, hq, hk, tables.shape[1], H.BLOCK)
+    assert (units + 7) // 8 * splits * batch > 512 and batch * splits <= 65536
+    print(f"decode work-item case {case}: hq {hq} hk {hk} {dtype} batch {batch} "
+          f"splits {splits} lens {lens}", flush=True)
+    query = H.randn(gen, (batch, hq, H.D), dtype)
+    seqlens = torch.tensor(lens, dtype=torch.int32)
+    scale = H.D ** -0.5
+    out = fp8_decode_attention(query.to(H.DEV), *caches, seqlens.to(H.DEV), tables.to(H.DEV), scale)
+    torch.cuda.synchronize()
+    kc, vc, ks, vs = H.cache_to_numpy(*caches)
+    ref = O.decode_attention(query, kc, vc, ks, vs, seqlens, tables, scale)
+    H.assert_attention_close(out, ref)
+    assert (out[seqlens.to(H.DEV) == 0] == 0).all()
 
 
 @pytest.mark.parametrize("case", range(8))
