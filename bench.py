@@ -700,18 +700,21 @@ def _unfused_prologue(positions, q, k, v, qw, kw, eps, cos, sin, cache, slots):
 
 def time_norm_rope(dev, iters=20, warmup=3):
     """Fused q/k RMSNorm + rotary + FP8 store against the reference's unfused
-    torch chain (plus the store kernel), Qwen3-8B heads, bf16."""
+    torch chain (plus the store kernel), Qwen3-8B heads: the prefill and
+    decode steps in bf16, and the prefill step in fp16, the activation type
+    the reference requires with an FP8 cache (Config.py:35-36)."""
     from microserve_amd import qk_norm_rope_store
     gen = torch.Generator().manual_seed(77)
-    cos_t, sin_t = _rope_tables_bf16(40960)
-    cos_t, sin_t = cos_t.to(dev), sin_t.to(dev)
     out = []
-    for n, mode in ((FRESH_SEQS * FRESH_LEN, "prefill"), (BATCH, "decode")):
-        qkv = torch.randn(n, (HQ + 2 * HK) * D, generator=gen).bfloat16().to(dev)
+    for n, mode, dt in ((FRESH_SEQS * FRESH_LEN, "prefill", torch.bfloat16),
+                        (BATCH, "decode", torch.bfloat16),
+                        (FRESH_SEQS * FRESH_LEN, "prefill", torch.float16)):
+        cos_t, sin_t = (t.to(dev) for t in _rope_tables(40960, dt))
+        qkv = torch.randn(n, (HQ + 2 * HK) * D, generator=gen).to(dt).to(dev)
         q, k, v = (t.view(n, -1, D) for t in qkv.split([HQ * D, HK * D, HK * D], dim=-1))
         pos = torch.randint(0, 40960, (n,), generator=gen).to(dev)
-        qw = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16().to(dev)
-        kw = (1 + 0.1 * torch.randn(D, generator=gen)).bfloat16().to(dev)
+        qw = (1 + 0.1 * torch.randn(D, generator=gen)).to(dt).to(dev)
+        kw = (1 + 0.1 * torch.randn(D, generator=gen)).to(dt).to(dev)
         nb = max(1, -(-n // BS))
         slots = torch.randperm(nb * BS, generator=gen)[:n].to(dev)
         cache = (torch.zeros(nb, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev),
@@ -743,8 +746,10 @@ def time_norm_rope(dev, iters=20, warmup=3):
             torch.cuda.synchronize()
             res[name] = e0.elapsed_time(e1) / iters * 1e3
         nbytes = norm_rope_bytes(n, HQ, HK, with_k)
-        cpu = _cpu_norm_rope(qkv, pos, qw, kw, cos_t, sin_t, slots, nb) if mode == "prefill" else None
-        out.append({"workload": f"{mode}: {n} tokens, 32 q / 8 kv heads, bf16, rotary table "
+        cpu = (_cpu_norm_rope(qkv, pos, qw, kw, cos_t, sin_t, slots, nb)
+               if mode == "prefill" and dt == torch.bfloat16 else None)
+        dname = "bf16" if dt == torch.bfloat16 else "fp16"
+        out.append({"workload": f"{mode}: {n} tokens, 32 q / 8 kv heads, {dname}, rotary table "
                                 f"40960 x 128",
                     "us": round(res["fused"], 2), "unfused_us": round(res["unfused"], 2),
                     "speedup": round(res["unfused"] / res["fused"], 2),
@@ -780,13 +785,13 @@ def _cpu_norm_rope(qkv, pos, qw, kw, cos_t, sin_t, slots, nb, sample=4096):
                                       f"on the host"}
 
 
-def _rope_tables_bf16(max_position, base=1e6):
+def _rope_tables(max_position, dtype, base=1e6):
     """cos/sin tables as the reference builds them (rotary_embedding.py:16-22)
     after the runner's cast to the activation type."""
     inv_freq = 1.0 / (base ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
     freqs = torch.einsum("i,j -> ij", torch.arange(max_position, dtype=torch.float32), inv_freq)
     emb = torch.cat((freqs, freqs), dim=-1)
-    return emb.cos().bfloat16(), emb.sin().bfloat16()
+    return emb.cos().to(dtype), emb.sin().to(dtype)
 
 
 def calibrate_copy(dev, nbytes=1 << 30, iters=5):

@@ -129,9 +129,11 @@ __device__ __forceinline__ void norm_rope_row(const NormRopeArgs& a, bool has_w,
                                               float* x) {
 #pragma clang fp contract(off)
   if (has_w) {
+    // each square is exact in fp32, so the fused multiply-add rounds the
+    // running sum exactly as a multiply and an add would
     float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) ss += x[i] * x[i];  // each square is exact
+    for (int i = 0; i < 16; ++i) ss = fmaf(x[i], x[i], ss);
     const float var = sum8_dpp(ss) / (float)kHeadDim;
     const float r = 1.0f / sqrtf(var + a.eps);
 #pragma unroll
@@ -159,6 +161,68 @@ __device__ __forceinline__ void store_fp8_row(const NormRopeArgs& a, bool is_v, 
   __builtin_nontemporal_store(u32x2{qb[2], qb[3]},
                               reinterpret_cast<u32x2*>(cache + dst * kHeadDim + hi));
   if (sub == 0) (is_v ? a.v_scale : a.k_scale)[dst] = scale;
+}
+
+// Bit casts between a 32-bit word and an fp16 pair, through a scalar copy:
+// clang lowers __builtin_bit_cast applied directly to an element of an
+// ext_vector_type value (v[i]) to element 0 for every index.
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t w) { return __builtin_bit_cast(f16x2, w); }
+__device__ __forceinline__ uint32_t as_u32(f16x2 h) { return __builtin_bit_cast(uint32_t, h); }
+
+// The fp16 form of norm_rope_row on packed pairs: xl / xh hold the lane's
+// 16 elements as fp16 pairs and come back holding the result.  Products of
+// two fp16 values are exact in fp32, and the sum of two fp16 values rounds
+// to the same fp16 whether or not it is first rounded to fp32 (when the
+// fp32 sum is inexact the smaller term is below an eighth of an fp16 ulp),
+// so v_pk_mul_f16 / v_pk_add_f16, which round once, give torch's
+// T(T(.) op T(.)) bit for bit with no round trip through fp32.  Only x * r
+// (r in fp32) is taken in fp32.
+__device__ __forceinline__ void norm_rope_row_f16(const NormRopeArgs& a, bool has_w,
+                                                  bool pos_ok, const f16x2* w2,
+                                                  const f16x2* c2, const f16x2* s2,
+                                                  u32x4& xl, u32x4& xh) {
+#pragma clang fp contract(off)
+  f16x2 y[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    y[i] = as_f16x2(xl[i]);
+    y[4 + i] = as_f16x2(xh[i]);
+  }
+  if (has_w) {
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[2 * i] = (float)y[i][0];
+      x[2 * i + 1] = (float)y[i][1];
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ss = fmaf(x[i], x[i], ss);
+    const float var = sum8_dpp(ss) / (float)kHeadDim;
+    const float r = 1.0f / sqrtf(var + a.eps);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float p0 = x[2 * i] * r, p1 = x[2 * i + 1] * r;
+      asm volatile("" : "+v"(p0), "+v"(p1));  // round x * r to fp32 first
+      y[i] = f16x2{(_Float16)p0, (_Float16)p1} * w2[i];
+    }
+  }
+  // lanes' pairs 0-3 are d in [8l, 8l+8), pairs 4-7 are d + 64
+  f16x2 o[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x2 a0 = y[i] * c2[i];
+    const f16x2 b0 = y[4 + i] * s2[i];
+    o[i] = a0 - b0;
+    const f16x2 a1 = y[4 + i] * c2[4 + i];
+    const f16x2 b1 = y[i] * s2[4 + i];
+    o[4 + i] = a1 + b1;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    xl[i] = pos_ok ? as_u32(o[i]) : 0u;
+    xh[i] = pos_ok ? as_u32(o[4 + i]) : 0u;
+  }
 }
 
 // Each 8-lane group owns one chunk: up to kNrChunk consecutive heads of one
@@ -204,6 +268,60 @@ __global__ __launch_bounds__(kNrThreads) void qk_norm_rope_store_kernel(NormRope
   // the cache takes k and v rows only at valid positions and slots
   const bool to_cache = kind != 0 && pos_ok && slot >= 0 && slot < a.num_slots;
   float x[16];
+  if constexpr (__is_same(T, _Float16)) {
+    if (kind != 2) {
+      const uint16_t* w = kind == 0 ? a.q_weight : a.k_weight;
+      const bool has_w = w != nullptr;
+      // the norm weights and the token's rotary values stay packed
+      f16x2 w2[8], c2[8], s2[8];
+      const int64_t tab = (pos_ok ? pos : 0) * kHeadDim;
+      const u32x4 cl = *reinterpret_cast<const u32x4*>(a.cos + tab + lo);
+      const u32x4 ch = *reinterpret_cast<const u32x4*>(a.cos + tab + hi);
+      const u32x4 sl = *reinterpret_cast<const u32x4*>(a.sin + tab + lo);
+      const u32x4 sh = *reinterpret_cast<const u32x4*>(a.sin + tab + hi);
+      u32x4 wl = {0u, 0u, 0u, 0u}, wh = {0u, 0u, 0u, 0u};
+      if (has_w) {
+        wl = *reinterpret_cast<const u32x4*>(w + lo);
+        wh = *reinterpret_cast<const u32x4*>(w + hi);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        c2[i] = as_f16x2(cl[i]);
+        c2[4 + i] = as_f16x2(ch[i]);
+        s2[i] = as_f16x2(sl[i]);
+        s2[4 + i] = as_f16x2(sh[i]);
+        w2[i] = as_f16x2(wl[i]);
+        w2[4 + i] = as_f16x2(wh[i]);
+      }
+#pragma unroll
+      for (int r = 0; r < kNrChunk; ++r) {
+        if (r >= n) break;
+        u32x4 ol = xl[r], oh = xh[r];
+        norm_rope_row_f16(a, has_w, pos_ok, w2, c2, s2, ol, oh);
+        uint16_t* dst = kind == 0
+                            ? a.q_out + (tok * a.hq + h0 + r) * kHeadDim
+                            : (a.k_out ? a.k_out + (tok * a.hk + h0 + r) * kHeadDim : nullptr);
+        if (dst) {
+          __builtin_nontemporal_store(ol, reinterpret_cast<u32x4*>(dst + lo));
+          __builtin_nontemporal_store(oh, reinterpret_cast<u32x4*>(dst + hi));
+        }
+        if (to_cache) {
+          unpack8<T>(ol, x);
+          unpack8<T>(oh, x + 8);
+          store_fp8_row(a, false, slot * a.hk + h0 + r, sub, x);
+        }
+      }
+    } else if (to_cache) {
+#pragma unroll
+      for (int r = 0; r < kNrChunk; ++r) {
+        if (r >= n) break;
+        unpack8<T>(xl[r], x);
+        unpack8<T>(xh[r], x + 8);
+        store_fp8_row(a, true, slot * a.hk + h0 + r, sub, x);
+      }
+    }
+    return;
+  }
   if (kind != 2) {
     const uint16_t* w = kind == 0 ? a.q_weight : a.k_weight;
     const bool has_w = w != nullptr;
