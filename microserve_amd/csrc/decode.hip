@@ -734,10 +734,10 @@ __global__ __launch_bounds__(kOrderThreads) void decode_order_kernel(
 static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
 
 // Whether a decode shape runs compacted work items longest-first: split
-// grids of many rounds (the 4-wave shape), where a long sequence
-// dispatched late sets the makespan and most workgroups are empty splits
-// (ragged batch 256: 433 against 454 us).  Shapes only, like every launch
-// choice here.
+// grids of many rounds (over kWideGridMax eight-wave workgroups), where a
+// long sequence dispatched late sets the makespan and most workgroups are
+// empty splits (ragged batch 256: 423-426 against 454-457 us).  Shapes
+// only, like every launch choice here.
 constexpr int64_t kOrderMaxEntries = 1 << 16;  // batch * splits
 static bool ordered_of(int batch, int hk, int qgroups, int splits) {
   const int64_t wide_wgs =
@@ -862,8 +862,10 @@ static int decode_checked(const void* query, const void* k_cache, const void* v_
   const int group = num_q_heads / num_kv_heads;
   if (head_dim != kHeadDim || block_size % kStep != 0 || (group > 16 && group % 16 != 0))
     return MSKV_EUNSUPPORTED;
-  // page offsets are 32-bit buffer offsets
+  // page offsets are 32-bit buffer offsets, and token counts up to twice a
+  // table's width (w * block_size + split_tokens) stay within int
   if ((int64_t)block_size * num_kv_heads * head_dim > 0x7FFFFFFFLL) return MSKV_EUNSUPPORTED;
+  if ((int64_t)max_blocks_per_seq * block_size >= (1LL << 30)) return MSKV_EUNSUPPORTED;
   if (num_splits != mskv_decode_num_splits(batch, num_q_heads, num_kv_heads,
                                            max_blocks_per_seq, block_size))
     return MSKV_EINVAL;
