@@ -495,16 +495,17 @@ FRESH_SEQS, FRESH_LEN = 8, 8192
 BF16_PEAK_TFLOPS = 2500.0
 
 
-def time_fresh_prefill(dev, iters=10, warmup=2):
+def time_fresh_prefill(dev, iters=10, warmup=2, dtype=torch.bfloat16):
     """Fresh PREFILL (unquantized q/k/v, causal, the flash_attn_varlen_func
     call of the FP8 path): 8 sequences x 8192 new tokens, 32 q / 8 kv heads,
-    bf16 N(0,1)."""
+    N(0,1) in bf16, or in fp16, the activation type the reference requires
+    with an FP8 cache (Config.py:35-36)."""
     from microserve_amd import varlen_attention
     gen = torch.Generator().manual_seed(88)
     n = FRESH_SEQS * FRESH_LEN
-    q = torch.randn(n, HQ, D, generator=gen).bfloat16().to(dev)
-    k = torch.randn(n, HK, D, generator=gen).bfloat16().to(dev)
-    v = torch.randn(n, HK, D, generator=gen).bfloat16().to(dev)
+    q = torch.randn(n, HQ, D, generator=gen).to(dtype).to(dev)
+    k = torch.randn(n, HK, D, generator=gen).to(dtype).to(dev)
+    v = torch.randn(n, HK, D, generator=gen).to(dtype).to(dev)
     cu = torch.arange(0, FRESH_SEQS + 1, dtype=torch.int32, device=dev) * FRESH_LEN
 
     def run():
@@ -524,8 +525,9 @@ def time_fresh_prefill(dev, iters=10, warmup=2):
     us = sum(a.elapsed_time(b) for a, b in evs) / iters * 1e3
     flop = prefill_flops(FRESH_SEQS, 0, FRESH_LEN, HQ, D)
     tflops = flop / us / 1e6
+    dname = "bf16" if dtype == torch.bfloat16 else "fp16"
     return {"workload": "fresh causal prefill, 8 seqs x 8192 tokens, 32 q / 8 kv heads, "
-                        "bf16 q/k/v (16-bit MFMA)",
+                        f"{dname} q/k/v (16-bit MFMA)",
             "us": round(us, 2), "flop": flop, "tflops": round(tflops, 1),
             "peak_tflops": BF16_PEAK_TFLOPS, "frac": round(tflops / BF16_PEAK_TFLOPS, 4)}
 
@@ -832,7 +834,7 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="time only the varlen chunked prefill workload")
     ap.add_argument("--prefill-dtype", choices=["bf16", "fp16"], default="bf16",
-                    help="activation type of the --prefill-only workload")
+                    help="activation type of the --prefill-only and --fresh-only workloads")
     ap.add_argument("--fresh-only", action="store_true",
                     help="time only the fresh (unquantized) prefill workload")
     ap.add_argument("--shapes-only", action="store_true",
@@ -859,7 +861,8 @@ def main():
                           "long_context": [time_long_context(dev, b) for b in (1, 2, 4)]}))
         return
     if args.fresh_only:
-        print(json.dumps({"fresh_prefill": time_fresh_prefill(dev)}))
+        dtype = torch.bfloat16 if args.prefill_dtype == "bf16" else torch.float16
+        print(json.dumps({"fresh_prefill": time_fresh_prefill(dev, dtype=dtype)}))
         return
     if args.norm_rope_only:
         print(json.dumps({"qk_norm_rope_store": time_norm_rope(dev)}))
@@ -949,6 +952,7 @@ def main():
         # cache (Config.py:35-36)
         result["prefill_fp16"] = time_prefill(dev, dtype=torch.float16)
         result["fresh_prefill"] = time_fresh_prefill(dev)
+        result["fresh_prefill_fp16"] = time_fresh_prefill(dev, dtype=torch.float16)
         del w
         torch.cuda.empty_cache()
         result["fp16"] = time_fp16(dev)
