@@ -94,6 +94,60 @@ def test_fused_store_equals_store_kernel_on_the_rotated_k(dtype, slot_dtype):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("with_norm", [True, False])
+def test_fused_prologue_edge_values(dtype, with_norm):
+    """Bit-exact at the edges of the 16-bit types, where the fp16 form's
+    packed multiplies and adds must round as torch's fp32 op + cast does:
+    rows of tiny magnitudes (the rotary products go subnormal), rows near
+    the type's largest values, signed zeros, rows of one repeated value,
+    and tiny / large norm weights; with and without the norm."""
+    hq, hk, n = 16, 8, 400
+    gen = torch.Generator().manual_seed(31 + with_norm)
+    heads = hq + 2 * hk
+    base = torch.randn(n, heads, D, generator=gen)
+    # large rows stay below max / 16, so a rotated sum cannot overflow; the
+    # smallest magnitudes give subnormal products (in fp16 the 1e-37 rows
+    # are zeros)
+    big = (6.0e4 if dtype == torch.float16 else 3.0e38) / 16
+    mag = torch.tensor([1.0, 1e-5, 3e-7, 6e-8, big / 4, 1e-37, 1e-3, 2.0])
+    rowscale = mag[torch.randint(0, len(mag), (n, heads), generator=gen)]
+    x = base * rowscale[..., None]
+    x[0::7, :, 5:9] = 0.0
+    x[1::7, :, 5:9] = -0.0
+    x[2::11] = 0.75                       # rows of one repeated value
+    qkv = x.reshape(n, heads * D).to(dtype)
+    pos = torch.randint(0, MAXPOS, (n,), generator=gen)
+    pos[:8] = torch.tensor([0, 1, 2, 3, MAXPOS - 1, MAXPOS - 2, 12345, 7])
+    slots = torch.randperm(64 * 256, generator=gen)[:n].long()
+    if with_norm:
+        qw = (1 + 0.2 * torch.randn(D, generator=gen))
+        qw[:4] = torch.tensor([1e-4, 3e-6, 50.0, -7.0])
+        kw = qw.flip(0).clone()
+        qw, kw = qw.to(dtype), kw.to(dtype)
+    else:
+        qw = kw = None
+    cos, sin = NR.rope_tables(MAXPOS, 1e6, dtype)
+    kc, vc, ks, vs = alloc_cache(64, kv_heads=hk)
+    q, k, v = _split(qkv.to(DEV), hq, hk)
+    q_out, k_out = qk_norm_rope_store(
+        pos.to(DEV), q, k, v, None if qw is None else qw.to(DEV),
+        None if kw is None else kw.to(DEV), EPS, cos.to(DEV), sin.to(DEV), kc, vc, ks, vs,
+        slots.to(DEV))
+    torch.cuda.synchronize()
+    qc, kcpu, vcpu = _split(qkv, hq, hk)
+    rq, rk = NR.qk_norm_rope(qc, kcpu, pos, qw, kw, EPS, cos, sin)
+    assert torch.isfinite(rq.float()).all() and torch.isfinite(rk.float()).all()
+    gq, gk = q_out.cpu(), k_out.cpu()
+    assert torch.equal(gq.view(torch.int16), rq.view(torch.int16)), "q bits differ"
+    assert torch.equal(gk.view(torch.int16), rk.view(torch.int16)), "k bits differ"
+    okc, ovc, oks, ovs = _oracle_cache(rk, vcpu, slots, 64, 256, hk)
+    assert np.array_equal(kc.view(torch.uint8).cpu().numpy(), okc), "k cache bytes differ"
+    assert np.array_equal(vc.view(torch.uint8).cpu().numpy(), ovc), "v cache bytes differ"
+    assert np.array_equal(ks.cpu().numpy(), oks) and np.array_equal(vs.cpu().numpy(), ovs)
+
+
+@pytest.mark.gpu
 def test_no_norm_no_k_and_invalid_positions():
     dtype, hq, hk, n = torch.bfloat16, 32, 8, 300
     qkv, pos, slots, qw, kw = _inputs(n, hq, hk, dtype, seed=21)
