@@ -61,8 +61,9 @@ def rms_norm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
     xf = x.float().reshape(-1, HEAD_DIM).numpy()
     lanes = xf[:, _lane_order()].reshape(-1, 8, 16)
     s = np.zeros(lanes.shape[:2], np.float32)
-    for i in range(16):
-        s = s + lanes[:, :, i] * lanes[:, :, i]
+    with np.errstate(over="ignore"):  # fp32 squares of huge rows overflow to inf, as IEEE does
+        for i in range(16):
+            s = s + lanes[:, :, i] * lanes[:, :, i]
     tot = ((s[:, 0] + s[:, 1]) + (s[:, 2] + s[:, 3])) + ((s[:, 4] + s[:, 5]) + (s[:, 6] + s[:, 7]))
     var = tot / np.float32(HEAD_DIM)
     r = np.float32(1.0) / np.sqrt(var + np.float32(eps))
