@@ -97,3 +97,24 @@ def test_fresh_prefill_batch_equals_alone_and_alias():
                                  causal=True)
     torch.cuda.synchronize()
     assert torch.equal(batch[33:183], one)
+
+
+HEADS = [(16, 16), (16, 8), (32, 8), (64, 8), (32, 2), (16, 1), (48, 8), (40, 8)]
+
+
+@pytest.mark.parametrize("case", range(8))
+def test_fresh_prefill_random_shapes(case):
+    """Seeded random sweep: batch, query and key lengths (zero, one, short,
+    multi-tile; Lk >= Lq, so the causal diagonal sits bottom-right), GQA
+    groups 1-16 including groups that do not divide 16, both 16-bit types."""
+    import random
+    rng = random.Random(7000 + case)
+    hq, hk = HEADS[case % len(HEADS)]
+    dtype = rng.choice([torch.bfloat16, torch.float16])
+    nseq = rng.randint(1, 6)
+    lq = [rng.choice([0, 1, rng.randint(2, 200), rng.randint(200, 900)]) for _ in range(nseq)]
+    lk = [q + rng.choice([0, 0, rng.randint(1, 700)]) for q in lq]
+    print(f"fresh prefill case {case}: hq {hq} hk {hk} {dtype} lq {lq} lk {lk}", flush=True)
+    q, k, v, cu_q, cu_k = _setup(8000 + case, lq, lk, hq, hk, dtype)
+    if sum(lq):
+        _check(q, k, v, cu_q, cu_k, [max(1, x) for x in lq], [max(1, x) for x in lk])
