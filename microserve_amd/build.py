@@ -36,7 +36,9 @@ HIP_FLAGS = [
 FILE_FLAGS = {
     "decode.hip": ["-fno-honor-nans"],
     "prefill.hip": ["-fno-honor-nans"],
-    "dense_prefill.hip": ["-fno-honor-nans"],
+    # the iterative min-register machine scheduler orders this kernel's
+    # MFMAs and softmax 1.2% faster than the default, with no spills
+    "dense_prefill.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-sched-strategy=iterative-minreg"],
 }
 
 
