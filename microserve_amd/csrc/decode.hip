@@ -359,11 +359,13 @@ __device__ __forceinline__ void write_partial(float* po, float* plse, const f32x
   if (g == 0) *plse = l > 0.0f ? m + __log2f(l) : -INFINITY;
 }
 
-// 3 waves per SIMD: the register budget (<= 168 VGPRs) that holds a whole
-// step in flight without spilling
+// 2 waves per SIMD, the occupancy the LDS allows: one 8-wave workgroup
+// (132 KB) or two 4-wave ones (66 KB each) per CU.  (A hint of 3 could not
+// be met and left the 4-wave instance at 200 VGPRs instead of 167, with no
+// difference in time.)
 template <typename T, int W>
 __global__ __launch_bounds__(64 * W)
-__attribute__((amdgpu_waves_per_eu(3, 8)))
+__attribute__((amdgpu_waves_per_eu(2, 8)))
 void decode_fp8_kernel(DecodeArgs a) {
   // per wave: two K/V tile pairs and their scales; step i is read from
   // buffer i&1 while step i+1 is staged into the other one

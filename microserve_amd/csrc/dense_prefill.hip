@@ -12,7 +12,7 @@
 //  * A workgroup is four waves over one (sequence, kv head, block of query
 //    tokens); each wave owns three 16-row blocks, a row being one (query
 //    token, q head) pair of the kv head's GQA group, so every K/V operand
-//    read from LDS feeds three MFMAs (236 VGPRs: two waves per SIMD, as the
+//    read from LDS feeds three MFMAs (244 VGPRs: two waves per SIMD, as the
 //    64 KB of LDS per workgroup allows; three blocks measured 6.7% faster
 //    than two).
 //  * K/V tiles of 64 keys (256-byte rows) are staged in LDS with direct
