@@ -244,7 +244,6 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
   }
 
   const uint32_t page_bytes = (uint32_t)a.bs * a.hk * kHeadDim;
-  const uint32_t spage_bytes = (uint32_t)a.bs * a.hk * 4u;
   const uint32_t rstride = (uint32_t)a.hk * kHeadDim;
   // the block table is read-only: the constant address space keeps its
   // loads scalar
