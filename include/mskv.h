@@ -166,9 +166,9 @@ int mskv_fp8_decode_attention_noalloc(const void* query, const void* k_cache,
  * every sequence's query count: it sizes the grid, and query rows past it
  * are not written (flash-attn's contract for the same argument).
  * Supported: head_dim == 128, block_size % 128 == 0, GQA group <= 16 or a
- * multiple of 16, num_seqs <= 65535, and max_seqlen_q <= 65535 query blocks
- * of 128 rows (2M tokens at GQA 4, 524k at GQA 16); MSKV_EUNSUPPORTED
- * otherwise.
+ * multiple of 16, num_seqs <= 65535, max_seqlen_q <= 65535 query blocks
+ * of 128 rows (2M tokens at GQA 4, 524k at GQA 16), and a positive, finite
+ * softmax_scale; MSKV_EUNSUPPORTED otherwise.
  */
 int mskv_fp8_prefill_attention(const void* query, const void* k_cache,
                                const void* v_cache, const float* k_scale_cache,
@@ -200,8 +200,9 @@ int mskv_fp8_prefill_attention(const void* query, const void* k_cache,
  * max_seqlen_q must be at least every sequence's query count: it sizes the
  * grid, and query rows past it are not written (as in flash-attn).
  * Supported: head_dim == 128, GQA group <= 16 or a multiple of 16,
- * num_seqs <= 65535, and max_seqlen_q <= 65535 query blocks of 192 rows
- * (3.1M tokens at GQA 4); MSKV_EUNSUPPORTED otherwise.
+ * num_seqs <= 65535, max_seqlen_q <= 65535 query blocks of 192 rows
+ * (3.1M tokens at GQA 4), and a positive, finite softmax_scale;
+ * MSKV_EUNSUPPORTED otherwise.
  */
 int mskv_prefill_attention(const void* query, const void* key,
                            const void* value, void* out,

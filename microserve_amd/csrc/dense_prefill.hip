@@ -219,22 +219,25 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
             if (key >= lim[b]) st[b][tt][r] = -INFINITY;
         }
     }
-    float tm[kDBlocks];
+    // Each lane tests its own 16 scores against the row's running max: a
+    // row's maximum is the largest of its four lanes', and the positive
+    // scale keeps the order, so the wave vote equals the test on the row
+    // maxima.  The cross-lane reduction runs only when the vote passes.
+    float lm[kDBlocks];
+    bool grow = false;
 #pragma unroll
     for (int b = 0; b < kDBlocks; ++b) {
       float v = fmaxf(fmaxf(st[b][0][0], st[b][0][1]), fmaxf(st[b][0][2], st[b][0][3]));
 #pragma unroll
       for (int tt = 1; tt < 4; ++tt)
         v = fmaxf(fmaxf(v, st[b][tt][0]), fmaxf(fmaxf(st[b][tt][1], st[b][tt][2]), st[b][tt][3]));
-      tm[b] = max_xor32(max_xor16(v)) * a.scale_log2;
+      lm[b] = v;
+      grow |= v * a.scale_log2 > m[b] + kDSlack;
     }
-    bool grow = false;
-#pragma unroll
-    for (int b = 0; b < kDBlocks; ++b) grow |= tm[b] > m[b] + kDSlack;
     if (__any(grow)) {
 #pragma unroll
       for (int b = 0; b < kDBlocks; ++b) {
-        const float m_new = fmaxf(m[b], tm[b]);
+        const float m_new = fmaxf(m[b], max_xor32(max_xor16(lm[b])) * a.scale_log2);
         const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[b] - m_new);
         lacc[b] *= alpha;
 #pragma unroll
@@ -350,6 +353,9 @@ extern "C" int mskv_prefill_attention(const void* query, const void* key, const 
   if (num_q_heads % num_kv_heads != 0) return MSKV_EINVAL;
   const int group = num_q_heads / num_kv_heads;
   if (head_dim != mskv::kHeadDim || (group > 16 && group % 16 != 0)) return MSKV_EUNSUPPORTED;
+  // the row maxima are taken before the scale, which must keep their order
+  const float scale_log2 = softmax_scale * mskv::kLog2e;
+  if (!(scale_log2 > 0.0f && scale_log2 < INFINITY)) return MSKV_EUNSUPPORTED;
   if (num_seqs == 0 || total_q == 0 || max_seqlen_q == 0) return MSKV_OK;
   if (!query || !key || !value || !out || !cu_seqlens_q || !cu_seqlens_k) return MSKV_EINVAL;
   // per-tile offsets are 32-bit: 64 key rows of all kv heads
@@ -370,7 +376,7 @@ extern "C" int mskv_prefill_attention(const void* query, const void* key, const 
   a.gc = group < 16 ? group : 16;
   a.qgroups = group <= 16 ? 1 : group / 16;
   a.tpr = 16 / a.gc;
-  a.scale_log2 = softmax_scale * mskv::kLog2e;
+  a.scale_log2 = scale_log2;
   const int per_wg = mskv::kDWaves * mskv::kDBlocks * a.tpr;
   // grid y and z are limited to 65535
   const int64_t qblocks = ((int64_t)max_seqlen_q + per_wg - 1) / per_wg;

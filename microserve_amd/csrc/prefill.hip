@@ -66,6 +66,14 @@ constexpr float kPVScaleMax = 128.0f;
 template <typename T> struct QuerySplit { static constexpr int parts = 3; };
 template <> struct QuerySplit<__bf16> { static constexpr int parts = 2; };
 
+// Whether the rescale test votes on lane maxima (skipping the cross-lane
+// reduction on tiles that need no rescale) or reduces every row first; the
+// two decide alike.  A/B builds on one box: the vote took the fp16 instance
+// 1.6% faster, but the bf16 instance, at the 256-VGPR limit, ran 1% slower
+// with it than with the reduction.
+template <typename T> struct RowVote { static constexpr bool on = true; };
+template <> struct RowVote<__bf16> { static constexpr bool on = false; };
+
 struct PrefillArgs {
   const uint16_t* q;
   const uint8_t* kc;
@@ -106,6 +114,7 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
   constexpr int NQ = QuerySplit<T>::parts;
   constexpr int kPBlocks = PShape::blocks;
   constexpr int kPWaves = PShape::waves;
+  constexpr bool kLaneVote = RowVote<T>::on;
   // two tile buffers as separate objects, and a loop unrolled by two, so
   // the compiler can see that the direct loads into one buffer never alias
   // the reads of the other (otherwise it waits for them before every read)
@@ -336,23 +345,37 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      // row maxima in log2 units (qs > 0 per row)
-      float tm[kPBlocks];
-#pragma unroll
-      for (int b = 0; b < kPBlocks; ++b) {
+      // Row maxima in log2 units (qs > 0 per row).  With kLaneVote each
+      // lane tests its own 32 scores against the row's running max: a row's
+      // maximum is the largest of its four lanes', and the positive scale
+      // keeps the order, so the wave vote equals the test on the row maxima,
+      // and the cross-lane reduction runs only when the vote passes.
+      auto lane_max = [&](int b) {
         float v = fmaxf(fmaxf(st[b][0][0], st[b][0][1]), fmaxf(st[b][0][2], st[b][0][3]));
 #pragma unroll
         for (int tt = 1; tt < 8; ++tt)
           v = fmaxf(fmaxf(v, st[b][tt][0]), fmaxf(fmaxf(st[b][tt][1], st[b][tt][2]), st[b][tt][3]));
-        tm[b] = max_xor32(max_xor16(v)) * qs[b];
-      }
+        return v;
+      };
+      float lm[kPBlocks];
       bool grow = false;
+      if constexpr (kLaneVote) {
 #pragma unroll
-      for (int b = 0; b < kPBlocks; ++b) grow |= tm[b] > m[b] + kPSlack;
+        for (int b = 0; b < kPBlocks; ++b) {
+          lm[b] = lane_max(b);
+          grow |= lm[b] * qs[b] > m[b] + kPSlack;
+        }
+      } else {
+#pragma unroll
+        for (int b = 0; b < kPBlocks; ++b) lm[b] = max_xor32(max_xor16(lane_max(b))) * qs[b];
+#pragma unroll
+        for (int b = 0; b < kPBlocks; ++b) grow |= lm[b] > m[b] + kPSlack;
+      }
       if (__any(grow)) {
 #pragma unroll
         for (int b = 0; b < kPBlocks; ++b) {
-          const float m_new = fmaxf(m[b], tm[b]);
+          const float tm = kLaneVote ? max_xor32(max_xor16(lm[b])) * qs[b] : lm[b];
+          const float m_new = fmaxf(m[b], tm);
           const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[b] - m_new);
           lacc[b] *= alpha;
 #pragma unroll
@@ -367,19 +390,24 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
       // with p <= 2^8 (the lazy rescale's slack) no weight leaves fp16's
       // range.  It only ever shrinks, and the accumulator is then rescaled
       // by the exact ratio; the output is divided by it at the end.
+      // A wave vote on the lanes' own keys skips the tile's v_scale maximum
+      // while every key fits under fw (a NaN scale fails the test and takes
+      // the exact path, whose maximum ignores it).
       {
-        float vm = fmaxf(vss[lane], vss[64 + lane]);
-        vm = max_xor32(max_xor16(max16_dpp(vm)));
-        if (vm > 0.0f && (fw == 0.0f || vm * fw > kPVScaleMax)) {
-          const float fnew = pow2_floor(kPVScaleMax / vm);
-          if (fw != 0.0f) {
-            const float r = fnew / fw;  // a power of two: exact
+        const float v0 = vss[lane], v1 = vss[64 + lane];
+        if (__any(!(v0 * fw <= kPVScaleMax) || !(v1 * fw <= kPVScaleMax)) || fw == 0.0f) {
+          const float vm = max_xor32(max_xor16(max16_dpp(fmaxf(v0, v1))));
+          if (vm > 0.0f && (fw == 0.0f || vm * fw > kPVScaleMax)) {
+            const float fnew = pow2_floor(kPVScaleMax / vm);
+            if (fw != 0.0f) {
+              const float r = fnew / fw;  // a power of two: exact
 #pragma unroll
-            for (int b = 0; b < kPBlocks; ++b)
+              for (int b = 0; b < kPBlocks; ++b)
 #pragma unroll
-              for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= r;
+                for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= r;
+            }
+            fw = fnew;
           }
-          fw = fnew;
         }
       }
       // fp16(v_scale * fw) of the tile's keys, computed once per key by
@@ -538,6 +566,9 @@ extern "C" int mskv_fp8_prefill_attention(
   if (head_dim != mskv::kHeadDim || block_size % mskv::kPStep != 0 ||
       (group > 16 && group % 16 != 0))
     return MSKV_EUNSUPPORTED;
+  // the row maxima are taken before the scale, which must keep their order
+  const float scale_log2 = softmax_scale * mskv::kLog2e;
+  if (!(scale_log2 > 0.0f && scale_log2 < INFINITY)) return MSKV_EUNSUPPORTED;
   if ((int64_t)block_size * num_kv_heads * head_dim > 0x7FFFFFFFLL) return MSKV_EUNSUPPORTED;
   if (num_seqs == 0 || total_q == 0 || max_seqlen_q == 0) return MSKV_OK;
   if (!query || !k_cache || !v_cache || !k_scale_cache || !v_scale_cache ||
@@ -566,7 +597,7 @@ extern "C" int mskv_fp8_prefill_attention(
   a.gc_magic = (256 + a.gc - 1) / a.gc;
   a.bs = block_size;
   a.w = max_blocks_per_seq;
-  a.scale_log2 = softmax_scale * mskv::kLog2e;
+  a.scale_log2 = scale_log2;
   const int per_wg = 8 * a.tpr;  // 128 rows: 8 blocks of 16 rows
   // grid y and z are limited to 65535
   const int64_t qblocks = ((int64_t)max_seqlen_q + per_wg - 1) / per_wg;

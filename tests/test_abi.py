@@ -89,6 +89,10 @@ def test_argument_validation_without_launch():
     big_q = 8 * 65535 + 1
     assert lib.mskv_fp8_prefill_attention(1, 1, 1, 1, 1, 1, None, None, 0, 1, 1, big_q, big_q, 128, 8, 128, 256, 10, 4, 0.1, 1, None) == EUNSUP
     assert lib.mskv_prefill_attention(1, 1, 1, 1, 1, 1, 1, big_q, big_q, 4 * 65535 * 48 + 1, 32, 8, 128, 0.1, 1, None) == EUNSUP
+    # prefills: the row maxima are taken before a positive, finite softmax scale
+    for sc in (0.0, -0.1, float("nan"), float("inf"), 3e38):
+        assert lib.mskv_fp8_prefill_attention(1, 1, 1, 1, 1, 1, None, None, 0, 1, 1, 10, 10, 32, 8, 128, 256, 10, 4, sc, 1, None) == EUNSUP
+        assert lib.mskv_prefill_attention(1, 1, 1, 1, 1, 1, 1, 10, 10, 10, 32, 8, 128, sc, 1, None) == EUNSUP
 
 
 def test_new_entry_points_validate_without_launch():
