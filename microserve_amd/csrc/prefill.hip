@@ -41,6 +41,7 @@
 //    longest workgroups of every sequence start before any shorter one.
 //    Pages are read through page-sized buffer resources; an invalid block
 //    id gives zero-length reads and its keys are masked.
+#include <float.h>
 #include <math.h>
 
 #include "mskv_device.h"
@@ -229,7 +230,10 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) acc[b][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     lacc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m[b] = -INFINITY;
+    // -FLT_MAX rather than -inf: a row that has seen no key yet keeps it,
+    // and its masked (-inf) scores still give p = 0 with no select; the
+    // first finite score raises it like any other growth
+    m[b] = -FLT_MAX;
   }
   float fw = 0.0f;
   f16x8 ones;
@@ -241,16 +245,13 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
   const uint32_t k_lo = tile_off(n, 2 * g), k_hi = tile_off(n, 2 * g + 1);
   // ds_read_b64_tr_b8 address of this lane for read qq (keys 8qq..8qq+7 of
   // the lane group's 32): key slot e = 8qq + i/2 maps to tile row
-  // 16*(e/4) + 4g + e%4, column half i%2
+  // 16*(e/4) + 4g + e%4, column half i%2.  Read qq's row is read 0's plus
+  // 32qq, so its address is read 0's plus 4096qq (an immediate offset), and
+  // bits 1-3 of the row, which select the swizzle, do not depend on qq.
   const int i16 = lane & 15;
-  uint32_t tr_row[4], tr_swz[4];
-#pragma unroll
-  for (int qq = 0; qq < 4; ++qq) {
-    const int e = 8 * qq + (i16 >> 1);
-    const int row = 16 * (e >> 2) + 4 * g + (e & 3);
-    tr_row[qq] = (uint32_t)row * kHeadDim + 8u * (i16 & 1);
-    tr_swz[qq] = 16u * (uint32_t)((row >> 1) & 7);
-  }
+  const int tr_r0 = 16 * (i16 >> 3) + 4 * g + ((i16 >> 1) & 3);
+  const uint32_t tr_row = (uint32_t)tr_r0 * kHeadDim + 8u * (i16 & 1);
+  const uint32_t tr_swz = 16u * (uint32_t)((tr_r0 >> 1) & 7);
 
   const uint32_t page_bytes = (uint32_t)a.bs * a.hk * kHeadDim;
   const uint32_t rstride = (uint32_t)a.hk * kHeadDim;
@@ -376,7 +377,7 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
         for (int b = 0; b < kPBlocks; ++b) {
           const float tm = kLaneVote ? max_xor32(max_xor16(lm[b])) * qs[b] : lm[b];
           const float m_new = fmaxf(m[b], tm);
-          const float alpha = m_new == -INFINITY ? 1.0f : exp2_fast(m[b] - m_new);
+          const float alpha = exp2_fast(m[b] - m_new);
           lacc[b] *= alpha;
 #pragma unroll
           for (int dt = 0; dt < 8; ++dt) acc[b][dt] *= alpha;
@@ -420,9 +421,6 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      float m_use[kPBlocks];
-#pragma unroll
-      for (int b = 0; b < kPBlocks; ++b) m_use[b] = m[b] == -INFINITY ? 0.0f : m[b];
       // The wave raises its priority over the P loop and the PV MFMAs and
       // drops it after.
       __builtin_amdgcn_s_setprio(1);
@@ -447,7 +445,7 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
           for (int b = 0; b < kPBlocks; ++b) {
             float pf[4];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) pf[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m_use[b]));
+            for (int r = 0; r < 4; ++r) pf[r] = exp2_fast(fmaf(st[b][tt][r], qs[b], -m[b]));
             const f16x2 p01 = {(_Float16)pf[0], (_Float16)pf[1]};
             const f16x2 p23 = {(_Float16)pf[2], (_Float16)pf[3]};
             const f16x2 w01 = p01 * f16x2{vf[0], vf[1]};
@@ -473,8 +471,8 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
       auto vread = [&](int dt, int c) {
         return __builtin_amdgcn_ds_read_tr8_b64_v2i32(
             reinterpret_cast<__attribute__((address_space(3))) i32x2*>(
-                (__attribute__((address_space(3))) uint8_t*)vt + tr_row[c] +
-                ((16u * dt) ^ tr_swz[c])));
+                (__attribute__((address_space(3))) uint8_t*)vt +
+                (tr_row + ((16u * dt) ^ tr_swz)) + 4096u * c));
       };
       i32x2 raw[4];
 #pragma unroll
