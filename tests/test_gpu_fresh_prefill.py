@@ -35,6 +35,17 @@ def _check(q, k, v, cu_q, cu_k, lq, lk):
     return H.assert_attention_close(out, ref), out
 
 
+@pytest.mark.parametrize("scale", [0.0, -0.088, float("nan"), float("inf")])
+def test_fresh_prefill_rejects_a_softmax_scale_that_is_not_positive(scale):
+    """The row maxima are taken before the softmax scale, so a scale that is
+    not positive and finite raises (MSKV_EUNSUPPORTED) instead of returning
+    rows normalized against the wrong maximum."""
+    q, k, v, cu_q, cu_k = _setup(6, [40], [40], 8, 2)
+    with pytest.raises(RuntimeError, match="status -2"):
+        varlen_attention(q.to(H.DEV), k.to(H.DEV), v.to(H.DEV), cu_q.to(H.DEV),
+                         cu_k.to(H.DEV), 40, 40, scale)
+
+
 def test_fresh_prefill_empty_sequences_and_oversized_max_seqlen():
     """Empty sequences at the start and in the middle of the batch, and
     max_seqlen_q far above the longest sequence."""

@@ -238,6 +238,20 @@ def test_varlen_prefill_empty_sequences_and_oversized_max_seqlen():
     H.assert_attention_close(out, ref)
 
 
+@pytest.mark.parametrize("scale", [0.0, -0.088, float("nan"), float("inf")])
+def test_prefill_rejects_a_softmax_scale_that_is_not_positive(scale):
+    """The row maxima are taken before the softmax scale, so a scale that is
+    not positive and finite raises (MSKV_EUNSUPPORTED) instead of returning
+    rows normalized against the wrong maximum."""
+    lq, lk = [20], [20 + 100]
+    query, tables, caches, cu_q, cu_k = _varlen_setup(233, lq, lk, 32, 8)
+    with pytest.raises(RuntimeError, match="status -2"):
+        fp8_varlen_prefill_attention(query.to(H.DEV), *caches, tables.to(H.DEV),
+                                     cu_q.to(H.DEV), cu_k.to(H.DEV), 20, scale)
+    with pytest.raises(RuntimeError, match="status -2"):
+        fp8_chunk_prefill_attention(query.to(H.DEV), *caches, tables.to(H.DEV), 100, scale)
+
+
 def test_chunk_prefill_single_equals_varlen():
     lq, lk = [100], [100 + 700]
     query, tables, caches, cu_q, cu_k = _varlen_setup(231, lq, lk, 32, 8)
