@@ -35,7 +35,9 @@ HIP_FLAGS = [
 # reference's whatever the input.
 FILE_FLAGS = {
     "decode.hip": ["-fno-honor-nans"],
-    "prefill.hip": ["-fno-honor-nans"],
+    # the max-ILP machine scheduler orders the FP8 prefill 1.5-2.3% faster
+    # than the default, with no spills
+    "prefill.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-sched-strategy=max-ilp"],
     # the iterative min-register machine scheduler orders this kernel's
     # MFMAs and softmax 1.2% faster than the default, with no spills
     "dense_prefill.hip": ["-fno-honor-nans", "-mllvm", "-amdgpu-sched-strategy=iterative-minreg"],

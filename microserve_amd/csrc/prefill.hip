@@ -67,14 +67,6 @@ constexpr float kPVScaleMax = 128.0f;
 template <typename T> struct QuerySplit { static constexpr int parts = 3; };
 template <> struct QuerySplit<__bf16> { static constexpr int parts = 2; };
 
-// Whether the rescale test votes on lane maxima (skipping the cross-lane
-// reduction on tiles that need no rescale) or reduces every row first; the
-// two decide alike.  A/B builds on one box: the vote took the fp16 instance
-// 1.6% faster, but the bf16 instance, at the 256-VGPR limit, ran 1% slower
-// with it than with the reduction.
-template <typename T> struct RowVote { static constexpr bool on = true; };
-template <> struct RowVote<__bf16> { static constexpr bool on = false; };
-
 struct PrefillArgs {
   const uint16_t* q;
   const uint8_t* kc;
@@ -115,7 +107,6 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
   constexpr int NQ = QuerySplit<T>::parts;
   constexpr int kPBlocks = PShape::blocks;
   constexpr int kPWaves = PShape::waves;
-  constexpr bool kLaneVote = RowVote<T>::on;
   // two tile buffers as separate objects, and a loop unrolled by two, so
   // the compiler can see that the direct loads into one buffer never alias
   // the reads of the other (otherwise it waits for them before every read)
@@ -346,37 +337,26 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      // Row maxima in log2 units (qs > 0 per row).  With kLaneVote each
-      // lane tests its own 32 scores against the row's running max: a row's
-      // maximum is the largest of its four lanes', and the positive scale
-      // keeps the order, so the wave vote equals the test on the row maxima,
-      // and the cross-lane reduction runs only when the vote passes.
-      auto lane_max = [&](int b) {
+      // Row maxima in log2 units (qs > 0 per row).  Each lane tests its own
+      // 32 scores against the row's running max: a row's maximum is the
+      // largest of its four lanes', and the positive scale keeps the order,
+      // so the wave vote equals the test on the row maxima, and the
+      // cross-lane reduction runs only when the vote passes.
+      float lm[kPBlocks];
+      bool grow = false;
+#pragma unroll
+      for (int b = 0; b < kPBlocks; ++b) {
         float v = fmaxf(fmaxf(st[b][0][0], st[b][0][1]), fmaxf(st[b][0][2], st[b][0][3]));
 #pragma unroll
         for (int tt = 1; tt < 8; ++tt)
           v = fmaxf(fmaxf(v, st[b][tt][0]), fmaxf(fmaxf(st[b][tt][1], st[b][tt][2]), st[b][tt][3]));
-        return v;
-      };
-      float lm[kPBlocks];
-      bool grow = false;
-      if constexpr (kLaneVote) {
-#pragma unroll
-        for (int b = 0; b < kPBlocks; ++b) {
-          lm[b] = lane_max(b);
-          grow |= lm[b] * qs[b] > m[b] + kPSlack;
-        }
-      } else {
-#pragma unroll
-        for (int b = 0; b < kPBlocks; ++b) lm[b] = max_xor32(max_xor16(lane_max(b))) * qs[b];
-#pragma unroll
-        for (int b = 0; b < kPBlocks; ++b) grow |= lm[b] > m[b] + kPSlack;
+        lm[b] = v;
+        grow |= v * qs[b] > m[b] + kPSlack;
       }
       if (__any(grow)) {
 #pragma unroll
         for (int b = 0; b < kPBlocks; ++b) {
-          const float tm = kLaneVote ? max_xor32(max_xor16(lm[b])) * qs[b] : lm[b];
-          const float m_new = fmaxf(m[b], tm);
+          const float m_new = fmaxf(m[b], max_xor32(max_xor16(lm[b])) * qs[b]);
           const float alpha = exp2_fast(m[b] - m_new);
           lacc[b] *= alpha;
 #pragma unroll
