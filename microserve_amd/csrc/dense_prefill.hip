@@ -34,7 +34,8 @@
 //    product whose V^T operand is all ones, so each output is an exact
 //    convex combination of V rows under the weights applied.
 //  * Online softmax in base 2 with a lazy rescale (slack 2^8; p <= 256 fits
-//    both fp16 and bf16); masks only on tiles that straddle the diagonal or
+//    both fp16 and bf16), decided by a wave vote on each lane's own scores
+//    before any cross-lane reduction; masks only on tiles that straddle the diagonal or
 //    the end of the keys; query blocks launch last-first across the whole
 //    grid.
 #include <math.h>

@@ -34,7 +34,9 @@
 //    softmax denominator is a ninth output tile: an all-ones A operand
 //    against the fp16 probabilities, summed in fp32 by the MFMA.
 //  * Online softmax in base 2 with a lazy rescale: the accumulator is
-//    rescaled only when some row's max grows by more than 2^8.  Masks are
+//    rescaled only when some row's max grows by more than 2^8, which a wave
+//    vote on each lane's own scores decides before any cross-lane
+//    reduction; the weight scale fw is checked the same way.  Masks are
 //    evaluated only on tiles that straddle the causal diagonal or the end
 //    of the keys; fully visible tiles skip them.
 //  * Query blocks are launched last-first across the whole grid, so the
