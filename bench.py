@@ -509,21 +509,33 @@ FRESH_SEQS, FRESH_LEN = 8, 8192
 BF16_PEAK_TFLOPS = 2500.0
 
 
-def time_fresh_prefill(dev, iters=20, warmup=30, dtype=torch.bfloat16):
-    """Fresh PREFILL (unquantized q/k/v, causal, the flash_attn_varlen_func
-    call of the FP8 path): 8 sequences x 8192 new tokens, 32 q / 8 kv heads,
-    N(0,1) in bf16, or in fp16, the activation type the reference requires
-    with an FP8 cache (Config.py:35-36)."""
-    from microserve_amd import varlen_attention
+def fresh_workload(dev, dtype=torch.bfloat16):
+    """Fresh PREFILL inputs: 8 sequences x 8192 new tokens, 32 q / 8 kv
+    heads, q/k/v N(0,1) in `dtype`, and their cu_seqlens."""
     gen = torch.Generator().manual_seed(88)
     n = FRESH_SEQS * FRESH_LEN
     q = torch.randn(n, HQ, D, generator=gen).to(dtype).to(dev)
     k = torch.randn(n, HK, D, generator=gen).to(dtype).to(dev)
     v = torch.randn(n, HK, D, generator=gen).to(dtype).to(dev)
     cu = torch.arange(0, FRESH_SEQS + 1, dtype=torch.int32, device=dev) * FRESH_LEN
+    return dict(q=q, k=k, v=v, cu=cu)
+
+
+def run_fresh_prefill(w):
+    from microserve_amd import varlen_attention
+    return varlen_attention(w["q"], w["k"], w["v"], w["cu"], w["cu"], FRESH_LEN, FRESH_LEN,
+                            D ** -0.5)
+
+
+def time_fresh_prefill(dev, iters=20, warmup=30, dtype=torch.bfloat16):
+    """Fresh PREFILL (unquantized q/k/v, causal, the flash_attn_varlen_func
+    call of the FP8 path): fresh_workload's 8 sequences x 8192 new tokens in
+    bf16, or in fp16, the activation type the reference requires with an
+    FP8 cache (Config.py:35-36)."""
+    w = fresh_workload(dev, dtype)
 
     def run():
-        return varlen_attention(q, k, v, cu, cu, FRESH_LEN, FRESH_LEN, D ** -0.5)
+        return run_fresh_prefill(w)
 
     us, us_cold = _time_sustained(run, iters, warmup)
     flop = prefill_flops(FRESH_SEQS, 0, FRESH_LEN, HQ, D)

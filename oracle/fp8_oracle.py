@@ -331,7 +331,7 @@ def chunk_prefill_attention(query, k_cache, v_cache, k_scale_cache,
 
 
 def dense_varlen_attention(query, key, value, cu_seqlens_q, cu_seqlens_k,
-                           softmax_scale) -> torch.Tensor:
+                           softmax_scale, rows=None) -> torch.Tensor:
     """Causal varlen attention over unquantized q/k/v, float32: the fresh
     PREFILL of the FP8 path, which the reference runs as
     ``flash_attn_varlen_func(q, k, v, ..., causal=True)`` on the new tokens
@@ -342,7 +342,9 @@ def dense_varlen_attention(query, key, value, cu_seqlens_q, cu_seqlens_k,
     causal mask is flash-attn's bottom-right alignment: query ``i`` sees key
     ``j`` iff ``j <= i + Lk - Lq`` (the same bound as the paged prefill's
     ``prefix + i + 1`` with ``prefix = Lk - Lq``).  Rows that see no key are
-    zero.  Returns float32 ``[total_q, H_q, D]``.
+    zero.  Returns float32 ``[total_q, H_q, D]``; with ``rows`` (ascending
+    query row indices into ``total_q``), only those rows,
+    ``[len(rows), H_q, D]``, each against the same keys as in the full result.
     """
     q = _as_t(query).float()
     k_all = _as_t(key).float()
@@ -352,21 +354,30 @@ def dense_varlen_attention(query, key, value, cu_seqlens_q, cu_seqlens_k,
     group = hq // hk
     cu_q = [int(x) for x in _as_t(cu_seqlens_q).reshape(-1).tolist()]
     cu_k = [int(x) for x in _as_t(cu_seqlens_k).reshape(-1).tolist()]
-    out = torch.zeros(tq, hq, d, dtype=torch.float32)
+    if rows is None:
+        sel_all = torch.arange(tq)
+    else:
+        sel_all = _as_t(rows, torch.int64).reshape(-1)
+        assert bool((sel_all[1:] > sel_all[:-1]).all()), "rows must be ascending"
+    out = torch.zeros(sel_all.numel(), hq, d, dtype=torch.float32)
     for s in range(len(cu_q) - 1):
         lq = cu_q[s + 1] - cu_q[s]
         lk = cu_k[s + 1] - cu_k[s]
         if lq <= 0 or lk <= 0:
             continue
+        at = ((sel_all >= cu_q[s]) & (sel_all < cu_q[s + 1])).nonzero().view(-1)
+        if at.numel() == 0:
+            continue
+        i = sel_all[at] - cu_q[s]  # query index in the sequence
         k = k_all[cu_k[s]:cu_k[s + 1]]
         v = v_all[cu_k[s]:cu_k[s + 1]]
-        qs = q[cu_q[s]:cu_q[s + 1]].view(lq, hk, group, d)
+        qs = q[cu_q[s] + i].view(i.numel(), hk, group, d)
         scores = torch.einsum("ikgd,lkd->kgil", qs, k) * softmax_scale
-        visible = torch.arange(lk)[None, :] <= (torch.arange(lq) + lk - lq)[:, None]
+        visible = torch.arange(lk)[None, :] <= (i + lk - lq)[:, None]
         scores = scores.masked_fill(~visible[None, None], float("-inf"))
         p = torch.nan_to_num(scores.softmax(-1), nan=0.0)  # rows that see nothing
         o = torch.einsum("kgil,lkd->ikgd", p, v)
-        out[cu_q[s]:cu_q[s + 1]] = o.reshape(lq, hq, d)
+        out[at] = o.reshape(i.numel(), hq, d)
     return out
 
 

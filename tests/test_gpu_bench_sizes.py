@@ -12,7 +12,14 @@
   bf16 and fp16: every output finite, and 512 query tokens per sequence (the
   first and last token of every 128-row workgroup block, the sequence's last
   token, the rest random) against the oracle over ``prefix + i + 1`` keys
-  (``fp8_chunk_prefill_attention.py:52-54``).
+  (``fp8_chunk_prefill_attention.py:52-54``);
+* the 8 x 8192 fresh prefill, bf16 and fp16: every output finite, and 512
+  query tokens per sequence (the first and last of every 192-row workgroup
+  block, the rest random) against the unquantized oracle over keys 0..i
+  (``attention.py:49-55``).
+
+The fill and decode check runs in bf16 and in fp16, the activation type
+the reference requires with an FP8 cache (``Config.py:35-36``).
 """
 
 import numpy as np
@@ -26,8 +33,9 @@ from tests import gpu_helpers as H
 pytestmark = pytest.mark.gpu
 
 
-def test_store_fill_qwen3_8b_every_byte_and_decode():
-    w = bench.build_workload(H.DEV)
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_store_fill_qwen3_8b_every_byte_and_decode(dtype):
+    w = bench.build_workload(H.DEV, dtype)
     torch.cuda.synchronize()
     kc8 = w["kc"].view(torch.uint8).view(-1, bench.HK, bench.D)
     vc8 = w["vc"].view(torch.uint8).view(-1, bench.HK, bench.D)
@@ -56,7 +64,7 @@ def test_store_fill_qwen3_8b_every_byte_and_decode():
         caches, tables = H.compact_cache((w["kc"], w["vc"], w["ks"], w["vs"]), w["tables"][half])
         ref = O.decode_attention(w["query"].cpu(), *caches, w["seqlens"].cpu(), tables, scale)
         max_abs, rel = H.assert_attention_close(out, ref)
-        print(f"decode half {half}: max_abs {max_abs:.3e} rel {rel:.3e}", flush=True)
+        print(f"decode {dtype} half {half}: max_abs {max_abs:.3e} rel {rel:.3e}", flush=True)
 
 
 def test_ragged_batch256_step_append_and_decode():
@@ -117,4 +125,22 @@ def test_chunked_prefill_full_size_sampled_rows(dtype):
                                      w["cu_k"].cpu(), bench.D ** -0.5, rows=rows)
     max_abs, rel = H.assert_attention_close(out[rows.to(H.DEV)], ref)
     print(f"prefill {dtype}: {rows.numel()} rows, max_abs {max_abs:.3e} rel {rel:.3e}",
+          flush=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_fresh_prefill_full_size_sampled_rows(dtype):
+    w = bench.fresh_workload(H.DEV, dtype)
+    out = bench.run_fresh_prefill(w)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()), "non-finite output"
+    # 192 rows of a workgroup block are 48 query tokens at GQA 4
+    assert bench.HQ // bench.HK == 4
+    rows = _sampled_rows(torch.Generator().manual_seed(6), bench.FRESH_SEQS, bench.FRESH_LEN,
+                         block_tokens=48)
+    assert rows.numel() == bench.FRESH_SEQS * 512
+    ref = O.dense_varlen_attention(w["q"].cpu(), w["k"].cpu(), w["v"].cpu(), w["cu"].cpu(),
+                                   w["cu"].cpu(), bench.D ** -0.5, rows=rows)
+    max_abs, rel = H.assert_attention_close(out[rows.to(H.DEV)], ref)
+    print(f"fresh prefill {dtype}: {rows.numel()} rows, max_abs {max_abs:.3e} rel {rel:.3e}",
           flush=True)

@@ -314,6 +314,11 @@ def test_dense_varlen_vs_loop_sdpa_and_paged_oracle():
     assert np.abs(a - b).max() < 1e-5
     # Lq > Lk: query i sees keys j <= i - 3; the first three rows see nothing
     assert np.all(a[12:15] == 0) and np.abs(a[15:18]).max() > 0
+    # rows=: a subset in every sequence, empty rows included, against the loop
+    rows = np.array([0, 3, 6, 8, 12, 14, 17])
+    sub = O.dense_varlen_attention(q, k, v, cu_q, cu_k, sc, rows=rows).numpy()
+    assert sub.shape == (rows.size, hq, d)
+    assert np.abs(sub - b[rows]).max() < 1e-5
     # square causal == SDPA is_causal (GQA expanded)
     qq = torch.from_numpy(q[0:7]).permute(1, 0, 2)[None]
     kk = torch.from_numpy(k[0:7]).permute(1, 0, 2).repeat_interleave(2, 0)[None]
