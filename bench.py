@@ -717,17 +717,19 @@ def _unfused_prologue(positions, q, k, v, qw, kw, eps, cos, sin, cache, slots):
     return q, k
 
 
-def time_norm_rope(dev, iters=20, warmup=3):
-    """Fused q/k RMSNorm + rotary + FP8 store against the reference's unfused
-    torch chain (plus the store kernel), Qwen3-8B heads: the prefill and
-    decode steps in bf16, and the prefill step in fp16, the activation type
-    the reference requires with an FP8 cache (Config.py:35-36)."""
-    from microserve_amd import qk_norm_rope_store
+NORM_ROPE_STEPS = ((FRESH_SEQS * FRESH_LEN, "prefill", torch.bfloat16),
+                   (BATCH, "decode", torch.bfloat16),
+                   (FRESH_SEQS * FRESH_LEN, "prefill", torch.float16))
+
+
+def norm_rope_workloads(dev, steps=len(NORM_ROPE_STEPS)):
+    """The fused prologue's inputs, Qwen3-8B heads, one dict per step of
+    NORM_ROPE_STEPS (the first `steps` of them, drawn in order from one
+    generator): q/k/v N(0,1) viewed from one [n, (32 + 2 * 8) * 128]
+    projection, random positions under 40960, weights 1 + N(0, 0.1), slots a
+    random permutation of a pool of ceil(n / 256) blocks."""
     gen = torch.Generator().manual_seed(77)
-    out = []
-    for n, mode, dt in ((FRESH_SEQS * FRESH_LEN, "prefill", torch.bfloat16),
-                        (BATCH, "decode", torch.bfloat16),
-                        (FRESH_SEQS * FRESH_LEN, "prefill", torch.float16)):
+    for n, mode, dt in NORM_ROPE_STEPS[:steps]:
         cos_t, sin_t = (t.to(dev) for t in _rope_tables(40960, dt))
         qkv = torch.randn(n, (HQ + 2 * HK) * D, generator=gen).to(dt).to(dev)
         q, k, v = (t.view(n, -1, D) for t in qkv.split([HQ * D, HK * D, HK * D], dim=-1))
@@ -739,6 +741,22 @@ def time_norm_rope(dev, iters=20, warmup=3):
         cache = (torch.zeros(nb, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev),
                  torch.zeros(nb, BS, HK, D, dtype=torch.float8_e4m3fn, device=dev),
                  torch.ones(nb, BS, HK, device=dev), torch.ones(nb, BS, HK, device=dev))
+        yield dict(n=n, mode=mode, dtype=dt, cos=cos_t, sin=sin_t, qkv=qkv, q=q, k=k, v=v,
+                   pos=pos, qw=qw, kw=kw, nb=nb, slots=slots, cache=cache)
+
+
+def time_norm_rope(dev, iters=20, warmup=3):
+    """Fused q/k RMSNorm + rotary + FP8 store against the reference's unfused
+    torch chain (plus the store kernel), Qwen3-8B heads: the prefill and
+    decode steps in bf16, and the prefill step in fp16, the activation type
+    the reference requires with an FP8 cache (Config.py:35-36)."""
+    from microserve_amd import qk_norm_rope_store
+    out = []
+    for w in norm_rope_workloads(dev):
+        n, mode, dt = w["n"], w["mode"], w["dtype"]
+        cos_t, sin_t, q, k, v, pos, qw, kw = (w[x] for x in
+                                              ("cos", "sin", "q", "k", "v", "pos", "qw", "kw"))
+        qkv, nb, slots, cache = w["qkv"], w["nb"], w["slots"], w["cache"]
         with_k = mode == "prefill"
 
         def fused():

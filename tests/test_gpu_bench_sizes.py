@@ -18,6 +18,10 @@
   block, the rest random) against the unquantized oracle over keys 0..i
   (``attention.py:49-55``).
 
+* the 65,536-token fused prologue steps, bf16 and fp16: q, k, every cache
+  byte and scale bit-exact against the oracle (``qwen3.py:49-53``,
+  ``fp8_kv_cache.py:24-39``).
+
 The fill and decode check runs in bf16 and in fp16, the activation type
 the reference requires with an FP8 cache (``Config.py:35-36``).
 """
@@ -144,3 +148,32 @@ def test_fresh_prefill_full_size_sampled_rows(dtype):
     max_abs, rel = H.assert_attention_close(out[rows.to(H.DEV)], ref)
     print(f"fresh prefill {dtype}: {rows.numel()} rows, max_abs {max_abs:.3e} rel {rel:.3e}",
           flush=True)
+
+
+@pytest.mark.parametrize("step", [0, 2])
+def test_fused_prologue_full_size_bit_exact(step):
+    """The 65,536-token prologue steps bench.py times (step 0 in bf16, step 2
+    in fp16): q, k, every cache byte and scale against the oracle."""
+    from microserve_amd import qk_norm_rope_store
+    from oracle import norm_rope_oracle as NR
+    for w in bench.norm_rope_workloads(H.DEV, steps=step + 1):
+        pass
+    assert w["n"] == 65536 and w["mode"] == "prefill"
+    q_out, k_out = qk_norm_rope_store(w["pos"], w["q"], w["k"], w["v"], w["qw"], w["kw"], 1e-6,
+                                      w["cos"], w["sin"], *w["cache"], w["slots"], return_k=True)
+    torch.cuda.synchronize()
+    rq, rk = NR.qk_norm_rope(w["q"].cpu(), w["k"].cpu(), w["pos"].cpu(), w["qw"].cpu(),
+                             w["kw"].cpu(), 1e-6, w["cos"].cpu(), w["sin"].cpu())
+    assert torch.equal(q_out.cpu(), rq), "q differs"
+    assert torch.equal(k_out.cpu(), rk), "k differs"
+    kq, kscale = H.oracle_quantize_threaded(rk)
+    vq, vscale = H.oracle_quantize_threaded(w["v"])
+    slots = w["slots"].cpu()
+    kc, vc, ks, vs = w["cache"]
+    assert np.array_equal(kc.view(torch.uint8).view(-1, bench.HK, bench.D)[slots].cpu().numpy(), kq)
+    assert np.array_equal(vc.view(torch.uint8).view(-1, bench.HK, bench.D)[slots].cpu().numpy(), vq)
+    assert np.array_equal(ks.view(-1, bench.HK)[slots].cpu().numpy().view(np.uint32),
+                          kscale.view(np.uint32))
+    assert np.array_equal(vs.view(-1, bench.HK)[slots].cpu().numpy().view(np.uint32),
+                          vscale.view(np.uint32))
+    print(f"fused prologue {w['dtype']}: {w['n']} tokens bit-exact", flush=True)
