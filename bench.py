@@ -473,11 +473,10 @@ def decode_bytes_ragged(lens, hq, hk, d, act_bytes=2):
     return kv + qo + tables
 
 
-def time_long_context(dev, batch, iters=50, warmup=5):
-    """Long-context decode at the Qwen3-32B shape: 64 q / 8 kv heads, every
-    sequence at context 131072 (512 blocks); two disjoint block sets
-    alternate between steps so the MALL cannot serve the reads."""
-    from microserve_amd import decode_num_splits, fp8_decode_attention
+def long_workload(dev, batch):
+    """Long-context decode inputs at the Qwen3-32B shape: 64 q / 8 kv heads,
+    every sequence at context 131072 (512 blocks), and two disjoint block
+    table sets over one filled pool."""
     gen = torch.Generator().manual_seed(5 + batch)
     hq, ctx = 64, 131072
     pages = ctx // BS
@@ -492,10 +491,21 @@ def time_long_context(dev, batch, iters=50, warmup=5):
             perm[batch * pages:].view(batch, pages).contiguous().to(dev)]
     seqlens = torch.full((batch,), ctx, dtype=torch.int32, device=dev)
     q = torch.randn(batch, hq, D, generator=gen).bfloat16().to(dev)
-    out = torch.empty_like(q)
+    return dict(q=q, kc=kc, vc=vc, ks=ks, vs=vs, seqlens=seqlens, tables=tabs, hq=hq, ctx=ctx,
+                pages=pages)
+
+
+def time_long_context(dev, batch, iters=50, warmup=5):
+    """Long-context decode (long_workload); the two block sets alternate
+    between steps so the MALL cannot serve the reads."""
+    from microserve_amd import decode_num_splits, fp8_decode_attention
+    w = long_workload(dev, batch)
+    hq, ctx, pages = w["hq"], w["ctx"], w["pages"]
+    out = torch.empty_like(w["q"])
 
     def step(i):
-        fp8_decode_attention(q, kc, vc, ks, vs, seqlens, tabs[i % 2], D ** -0.5, out=out)
+        fp8_decode_attention(w["q"], w["kc"], w["vc"], w["ks"], w["vs"], w["seqlens"],
+                             w["tables"][i % 2], D ** -0.5, out=out)
 
     us = _time_steps(step, iters, warmup)
     nbytes = decode_bytes(batch, ctx, hq, HK, D)

@@ -18,6 +18,8 @@
   block, the rest random) against the unquantized oracle over keys 0..i
   (``attention.py:49-55``).
 
+* the Qwen3-32B 131072-token decode at batch 2 and 4, both block table
+  sets, against the oracle's decode (``fp8_decode_attention.py:16-58``);
 * the 65,536-token fused prologue steps, bf16 and fp16: q, k, every cache
   byte and scale bit-exact against the oracle (``qwen3.py:49-53``,
   ``fp8_kv_cache.py:24-39``).
@@ -177,3 +179,22 @@ def test_fused_prologue_full_size_bit_exact(step):
     assert np.array_equal(vs.view(-1, bench.HK)[slots].cpu().numpy().view(np.uint32),
                           vscale.view(np.uint32))
     print(f"fused prologue {w['dtype']}: {w['n']} tokens bit-exact", flush=True)
+
+
+@pytest.mark.parametrize("batch", [2, 4])
+def test_long_context_decode_full_size(batch):
+    """The Qwen3-32B 131072-token decode bench.py times at batch 2 and 4
+    (128 splits per sequence), both block table sets, against the oracle's
+    decode (``fp8_decode_attention.py:16-58``)."""
+    from microserve_amd import fp8_decode_attention
+    w = bench.long_workload(H.DEV, batch)
+    scale = bench.D ** -0.5
+    for half in range(2):
+        out = fp8_decode_attention(w["q"], w["kc"], w["vc"], w["ks"], w["vs"], w["seqlens"],
+                                   w["tables"][half], scale)
+        torch.cuda.synchronize()
+        caches, tables = H.compact_cache((w["kc"], w["vc"], w["ks"], w["vs"]), w["tables"][half])
+        ref = O.decode_attention(w["q"].cpu(), *caches, w["seqlens"].cpu(), tables, scale)
+        max_abs, rel = H.assert_attention_close(out, ref)
+        print(f"131k decode batch {batch} half {half}: max_abs {max_abs:.3e} rel {rel:.3e}",
+              flush=True)
