@@ -28,6 +28,8 @@ extern "C" {
 /* activation element types (query, key, value, output) */
 #define MSKV_FLOAT16 0
 #define MSKV_BFLOAT16 1
+/* also accepted for the key/value rows of mskv_store_fp8_kvcache only */
+#define MSKV_FLOAT32 2
 /* slot_mapping element types */
 #define MSKV_INT32 0
 #define MSKV_INT64 1
@@ -51,9 +53,10 @@ const char* mskv_status_string(int status);
  * (kernel :11-39): scale = max(amax_d |x|, 1e-8) / 448, byte =
  * e4m3fn(clamp(x / scale, -448, 448)) with IEEE fp32 division, written at
  * cache row slot_mapping[t].  key/value: [num_tokens, num_kv_heads, head_dim]
- * in act_dtype.  Slots outside [0, num_slots) are skipped (num_slots =
- * num_blocks * block_size); the reference never produces them.
- * Supported: head_dim == 128.
+ * in act_dtype: MSKV_FLOAT16, MSKV_BFLOAT16 or MSKV_FLOAT32 (the reference
+ * upcasts any float input to fp32, :22-23).  Slots outside [0, num_slots)
+ * are skipped (num_slots = num_blocks * block_size); the reference never
+ * produces them.  Supported: head_dim == 128.
  */
 int mskv_store_fp8_kvcache(const void* key, const void* value,
                            void* k_cache, void* v_cache,
@@ -124,8 +127,9 @@ int mskv_fp8_decode_attention(const void* query, const void* k_cache,
  * rejected with MSKV_EWORKSPACE (e.g. batch 64 x 4096 tokens at 32 q heads
  * needs 4.2 MB, batch 4 x 131072 at 64 q heads 16.9 MB).  The call makes no
  * hipMalloc/hipFree; the array's address on the current device is looked
- * up once, on that device's first call.  No part of the array needs to
- * start at zero.  Every call on one GPU shares that GPU's array: calls that
+ * up once, on that device's first call, which must therefore be an eager
+ * call (not one under graph capture); later calls may be captured.  No part
+ * of the array needs to start at zero.  Every call on one GPU shares that GPU's array: calls that
  * may overlap on one GPU (different streams, or one graph replayed while
  * another call runs) race on it and must be serialized by the caller.
  * Arguments and results are mskv_fp8_decode_attention's.

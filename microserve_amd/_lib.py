@@ -16,6 +16,7 @@ LIB_PATH = os.path.join(_HERE, "libmskv.so")
 
 FLOAT16 = 0
 BFLOAT16 = 1
+FLOAT32 = 2  # key/value rows of the store only
 INT32 = 0
 INT64 = 1
 
@@ -92,6 +93,17 @@ def act_dtype(t) -> int:
     if t.dtype == torch.bfloat16:
         return BFLOAT16
     raise AssertionError(f"activation dtype must be float16 or bfloat16, got {t.dtype}")
+
+
+def store_dtype(t) -> int:
+    """Element type of the store's key/value rows: fp16, bf16 or fp32 (the
+    reference upcasts any float input to fp32, fp8_kv_cache.py:22-23)."""
+    import torch
+    if t.dtype == torch.float32:
+        return FLOAT32
+    if t.dtype in (torch.float16, torch.bfloat16):
+        return act_dtype(t)
+    raise AssertionError(f"key/value dtype must be float16, bfloat16 or float32, got {t.dtype}")
 
 
 def on_device(what: str, ref, *tensors) -> None:

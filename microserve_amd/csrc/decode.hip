@@ -213,18 +213,21 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int kvh
     }
     const bool vtok = lane >= 32 && lane - 32 < s.valid;
     if (__any(vtok && !(s.vscale * f <= kPvScaleMax)) || f == 0.0f) {
-      // first step, or a valid token whose weight could leave fp16's range:
-      // f from the largest v_scale of the step's valid tokens (and those
-      // before it), never growing
+      // no scale yet, or a valid token whose weight could leave fp16's
+      // range: f from the largest v_scale of the step's valid tokens (and
+      // those before it), never growing.  A step with no valid token (an
+      // invalid page, say) leaves f at 0, so that the first step that has
+      // one picks it: its tokens' weights are 0 meanwhile, which is what
+      // they contribute.
       float vm = vtok ? s.vscale : 0.0f;
       vm = fmaxf(max_xor32(max_xor16(max16_dpp(vm))), vseen);
-      const float fnew = vm > 0.0f ? pow2_floor(kPvScaleMax / vm) : 1.0f;
+      const float fnew = vm > 0.0f ? pow2_floor(kPvScaleMax / vm) : 0.0f;
       if (f != 0.0f && fnew < f) {
         const float r = fnew / f;  // a power of two < 1: exact
 #pragma unroll
         for (int dt = 0; dt < 8; ++dt) acc[dt] *= r;
       }
-      if (f == 0.0f || fnew < f) f = fnew;
+      if (fnew > 0.0f && (f == 0.0f || fnew < f)) f = fnew;
       vseen = vm;
     }
     s_lds[buf][lane] = lane < 32 ? s.kscale * a.scale_log2 : s.vscale * f;
@@ -733,7 +736,9 @@ __global__ __launch_bounds__(kOrderThreads) void decode_order_kernel(
     items[first + sp] = int4{b, sp, len_b, bt[(int64_t)b * w + sp * pages_per_split]};
 }
 
-static int qgroups_of(int group) { return group <= 16 ? 1 : group / 16; }
+// units of up to 16 q heads per kv head: a group above 16 that is not a
+// multiple of 16 leaves the last unit's surplus lanes idle (head_ok false)
+static int qgroups_of(int group) { return (group + 15) / 16; }
 
 // Whether a decode shape runs compacted work items longest-first: split
 // grids of many rounds (over kWideGridMax eight-wave workgroups), where a
@@ -862,8 +867,7 @@ static int decode_checked(const void* query, const void* k_cache, const void* v_
   if (act_dtype != MSKV_FLOAT16 && act_dtype != MSKV_BFLOAT16) return MSKV_EINVAL;
   if (num_q_heads % num_kv_heads != 0) return MSKV_EINVAL;
   const int group = num_q_heads / num_kv_heads;
-  if (head_dim != kHeadDim || block_size % kStep != 0 || (group > 16 && group % 16 != 0))
-    return MSKV_EUNSUPPORTED;
+  if (head_dim != kHeadDim || block_size % kStep != 0) return MSKV_EUNSUPPORTED;
   // page offsets are 32-bit buffer offsets, and token counts up to twice a
   // table's width (w * block_size + split_tokens) stay within int
   if ((int64_t)block_size * num_kv_heads * head_dim > 0x7FFFFFFFLL) return MSKV_EUNSUPPORTED;

@@ -137,7 +137,9 @@ __global__ __launch_bounds__(kDThreads, 2) void dense_prefill_kernel(DenseArgs a
 #pragma unroll
   for (int b = 0; b < kDBlocks; ++b) {
     const int qi = w_q0 + b * a.tpr + n / a.gc;
-    row_ok[b] = n < a.tpr * a.gc && qi < lq;
+    // a unit of a group above 16 that is not a multiple of 16 has idle
+    // lanes past the group's last head
+    row_ok[b] = n < a.tpr * a.gc && qi < lq && qgi * 16 + n % a.gc < a.group;
     qh[b] = kvh * a.group + qgi * 16 + n % a.gc;
     lim[b] = row_ok[b] ? qi + shift + 1 : 0;
     // B operand of S^T = K . Q^T: lane (g, n) holds d in [32c + 8g, +8)
@@ -353,7 +355,7 @@ extern "C" int mskv_prefill_attention(const void* query, const void* key, const 
   if (act_dtype != MSKV_FLOAT16 && act_dtype != MSKV_BFLOAT16) return MSKV_EINVAL;
   if (num_q_heads % num_kv_heads != 0) return MSKV_EINVAL;
   const int group = num_q_heads / num_kv_heads;
-  if (head_dim != mskv::kHeadDim || (group > 16 && group % 16 != 0)) return MSKV_EUNSUPPORTED;
+  if (head_dim != mskv::kHeadDim) return MSKV_EUNSUPPORTED;
   // the row maxima are taken before the scale, which must keep their order
   const float scale_log2 = softmax_scale * mskv::kLog2e;
   if (!(scale_log2 > 0.0f && scale_log2 < INFINITY)) return MSKV_EUNSUPPORTED;
@@ -375,7 +377,7 @@ extern "C" int mskv_prefill_attention(const void* query, const void* key, const 
   a.hk = num_kv_heads;
   a.group = group;
   a.gc = group < 16 ? group : 16;
-  a.qgroups = group <= 16 ? 1 : group / 16;
+  a.qgroups = (group + 15) / 16;
   a.tpr = 16 / a.gc;
   a.scale_log2 = scale_log2;
   const int per_wg = mskv::kDWaves * mskv::kDBlocks * a.tpr;

@@ -29,8 +29,11 @@
 //    P^T, so probabilities never move between lanes; V^T comes out of LDS
 //    with ds_read_b64_tr_b8 and converts to fp16 exactly.  Each weight is
 //    fp16(p) * fp16(v_scale * fw) (v_pk_mul_f16), fw a per-wave power of
-//    two set from the largest v_scale seen, so the weights keep 11
-//    significant bits whatever the spread of v_scale inside a tile.  The
+//    two set from the largest v_scale seen (it only shrinks).  A key whose
+//    v_scale lies within 2^21 of that largest one gets a normal fp16 scale
+//    (11 significant bits), however the scales spread inside a tile; one
+//    further below gets a subnormal scale, with fewer bits (and below
+//    ~2^32, zero), and a small p lowers that bound further.  The
 //    softmax denominator is a ninth output tile: an all-ones A operand
 //    against the fp16 probabilities, summed in fp32 by the MFMA.
 //  * Online softmax in base 2 with a lazy rescale: the accumulator is
@@ -165,7 +168,9 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
   for (int b = 0; b < kPBlocks; ++b) {
     const int nq = (n * a.gc_magic) >> 8;  // n / gc
     const int qi = w_q0 + b * a.tpr + nq;
-    row_ok[b] = n < a.tpr * a.gc && qi < lq;
+    // a unit of a group above 16 that is not a multiple of 16 has idle
+    // lanes past the group's last head
+    row_ok[b] = n < a.tpr * a.gc && qi < lq && qgi * 16 + n - nq * a.gc < a.group;
     qh[b] = kvh * a.group + qgi * 16 + n - nq * a.gc;
     lim[b] = row_ok[b] ? prefix + qi + 1 : 0;
     // lane (g, n) holds d in [32g, 32g+32) of its row
@@ -371,7 +376,8 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
       // pairs by v_pk_mul_f16.  fw is a power of two per wave, set from the
       // largest v_scale the wave has seen: v_scale * fw <= kPVScaleMax, so
       // with p <= 2^8 (the lazy rescale's slack) no weight leaves fp16's
-      // range.  It only ever shrinks, and the accumulator is then rescaled
+      // range (the bound on the smaller keys' precision is in the header).
+      // It only ever shrinks, and the accumulator is then rescaled
       // by the exact ratio; the output is divided by it at the end.
       // A wave vote on the lanes' own keys skips the tile's v_scale maximum
       // while every key fits under fw (a NaN scale fails the test and takes
@@ -508,7 +514,7 @@ __global__ __launch_bounds__(PShape::threads, 2) void prefill_fp8_kernel(Prefill
     const float lt = lacc[b][0];
     const int nq = (n_out * a.gc_magic) >> 8;  // n / gc
     const int qi = w_q0 + b * a.tpr + nq;
-    if (!(n_out < a.tpr * a.gc && qi < lq)) continue;
+    if (!(n_out < a.tpr * a.gc && qi < lq && qgi * 16 + n_out - nq * a.gc < a.group)) continue;
     // acc is in units of fw (a power of two): 1 / fw is exact
     const float scale = lt > 0.0f && fw > 0.0f ? (1.0f / lt) * (1.0f / fw) : 0.0f;
     const int qhb = kvh * a.group + qgi * 16 + n_out - nq * a.gc;
@@ -543,9 +549,7 @@ extern "C" int mskv_fp8_prefill_attention(
   if (cu_seqlens_q == nullptr && num_seqs != 1) return MSKV_EINVAL;
   if (cu_seqlens_q == nullptr && total_q > 0x7FFFFFFFLL - prefix_len) return MSKV_EINVAL;
   const int group = num_q_heads / num_kv_heads;
-  if (head_dim != mskv::kHeadDim || block_size % mskv::kPStep != 0 ||
-      (group > 16 && group % 16 != 0))
-    return MSKV_EUNSUPPORTED;
+  if (head_dim != mskv::kHeadDim || block_size % mskv::kPStep != 0) return MSKV_EUNSUPPORTED;
   // the row maxima are taken before the scale, which must keep their order
   const float scale_log2 = softmax_scale * mskv::kLog2e;
   if (!(scale_log2 > 0.0f && scale_log2 < INFINITY)) return MSKV_EUNSUPPORTED;
@@ -572,7 +576,7 @@ extern "C" int mskv_fp8_prefill_attention(
   a.hk = num_kv_heads;
   a.group = group;
   a.gc = group < 16 ? group : 16;
-  a.qgroups = group <= 16 ? 1 : group / 16;
+  a.qgroups = (group + 15) / 16;
   a.tpr = 16 / a.gc;
   a.gc_magic = (256 + a.gc - 1) / a.gc;
   a.bs = block_size;

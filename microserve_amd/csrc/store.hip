@@ -20,21 +20,38 @@ constexpr int kStoreLanesPerRow = kHeadDim / 16;  // 8
 constexpr int kStoreThreads = 256;
 constexpr int kStoreRowsPerBlock = kStoreThreads / kStoreLanesPerRow;
 
+// This lane's 16 elements of row `row` as fp32 (streaming loads: each row
+// is read once).  16-bit inputs convert exactly; fp32 inputs are used as
+// they are, as the reference's upcast leaves them.
 template <typename T>
-__device__ __forceinline__ void unpack16(const u32x4& a, const u32x4& b,
-                                         float* x) {
+__device__ __forceinline__ void load16(const void* base, int64_t row, int sub, float* x) {
+  if constexpr (sizeof(T) == 4) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const float*>(base) + row * kHeadDim + sub * 16);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    x[2 * i] = Act<T>::to_f32((uint16_t)(a[i] & 0xFFFFu));
-    x[2 * i + 1] = Act<T>::to_f32((uint16_t)(a[i] >> 16));
-    x[8 + 2 * i] = Act<T>::to_f32((uint16_t)(b[i] & 0xFFFFu));
-    x[8 + 2 * i + 1] = Act<T>::to_f32((uint16_t)(b[i] >> 16));
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 v = __builtin_nontemporal_load(p + c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[4 * c + i] = __uint_as_float(v[i]);
+    }
+  } else {
+    const u32x4* p = reinterpret_cast<const u32x4*>(
+        reinterpret_cast<const uint16_t*>(base) + row * kHeadDim + sub * 16);
+    const u32x4 a = __builtin_nontemporal_load(p);
+    const u32x4 b = __builtin_nontemporal_load(p + 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = Act<T>::to_f32((uint16_t)(a[i] & 0xFFFFu));
+      x[2 * i + 1] = Act<T>::to_f32((uint16_t)(a[i] >> 16));
+      x[8 + 2 * i] = Act<T>::to_f32((uint16_t)(b[i] & 0xFFFFu));
+      x[8 + 2 * i + 1] = Act<T>::to_f32((uint16_t)(b[i] >> 16));
+    }
   }
 }
 
 template <typename T, typename SlotT>
 __global__ __launch_bounds__(kStoreThreads) void store_fp8_kernel(
-    const uint16_t* __restrict__ key, const uint16_t* __restrict__ value,
+    const void* __restrict__ key, const void* __restrict__ value,
     uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
     float* __restrict__ k_scale, float* __restrict__ v_scale,
     const SlotT* __restrict__ slots, int64_t rows, int num_kv_heads,
@@ -47,18 +64,11 @@ __global__ __launch_bounds__(kStoreThreads) void store_fp8_kernel(
   const int head = (int)(row - tok * num_kv_heads);
   const int64_t slot = (int64_t)slots[tok];
 
-  const u32x4* kp = reinterpret_cast<const u32x4*>(key + row * kHeadDim + sub * 16);
-  const u32x4* vp = reinterpret_cast<const u32x4*>(value + row * kHeadDim + sub * 16);
-  const u32x4 k0 = __builtin_nontemporal_load(kp);
-  const u32x4 k1 = __builtin_nontemporal_load(kp + 1);
-  const u32x4 v0 = __builtin_nontemporal_load(vp);
-  const u32x4 v1 = __builtin_nontemporal_load(vp + 1);
-
   float x[16];
   u32x4 kq, vq;
-  unpack16<T>(k0, k1, x);
+  load16<T>(key, row, sub, x);
   const float ks = quantize16(x, kq);
-  unpack16<T>(v0, v1, x);
+  load16<T>(value, row, sub, x);
   const float vs = quantize16(x, vq);
 
   if (slot < 0 || slot >= num_slots) return;
@@ -84,14 +94,12 @@ static hipError_t launch_store(const void* key, const void* value, void* kc,
   const int64_t blocks = (rows + kStoreRowsPerBlock - 1) / kStoreRowsPerBlock;
   if (slot_dtype == MSKV_INT64)
     hipLaunchKernelGGL((store_fp8_kernel<T, int64_t>), dim3((unsigned)blocks),
-                       dim3(kStoreThreads), 0, stream, (const uint16_t*)key,
-                       (const uint16_t*)value, (uint8_t*)kc, (uint8_t*)vc, ks,
-                       vs, (const int64_t*)slots, rows, hk, num_slots);
+                       dim3(kStoreThreads), 0, stream, key, value, (uint8_t*)kc,
+                       (uint8_t*)vc, ks, vs, (const int64_t*)slots, rows, hk, num_slots);
   else
     hipLaunchKernelGGL((store_fp8_kernel<T, int32_t>), dim3((unsigned)blocks),
-                       dim3(kStoreThreads), 0, stream, (const uint16_t*)key,
-                       (const uint16_t*)value, (uint8_t*)kc, (uint8_t*)vc, ks,
-                       vs, (const int32_t*)slots, rows, hk, num_slots);
+                       dim3(kStoreThreads), 0, stream, key, value, (uint8_t*)kc,
+                       (uint8_t*)vc, ks, vs, (const int32_t*)slots, rows, hk, num_slots);
   return hipGetLastError();
 }
 
@@ -107,7 +115,8 @@ extern "C" int mskv_store_fp8_kvcache(const void* key, const void* value,
                                       int act_dtype, void* stream) {
   if (num_tokens < 0 || num_kv_heads <= 0 || num_slots < 0) return MSKV_EINVAL;
   if (slot_dtype != MSKV_INT32 && slot_dtype != MSKV_INT64) return MSKV_EINVAL;
-  if (act_dtype != MSKV_FLOAT16 && act_dtype != MSKV_BFLOAT16) return MSKV_EINVAL;
+  if (act_dtype != MSKV_FLOAT16 && act_dtype != MSKV_BFLOAT16 && act_dtype != MSKV_FLOAT32)
+    return MSKV_EINVAL;
   if (head_dim != mskv::kHeadDim) return MSKV_EUNSUPPORTED;
   if (num_tokens == 0) return MSKV_OK;
   if (!key || !value || !k_cache || !v_cache || !k_scale_cache ||
@@ -117,15 +126,18 @@ extern "C" int mskv_store_fp8_kvcache(const void* key, const void* value,
           mskv::kStoreRowsPerBlock > 0x7FFFFFFFLL)
     return MSKV_EUNSUPPORTED;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e =
-      act_dtype == MSKV_BFLOAT16
-          ? mskv::launch_store<__bf16>(key, value, k_cache, v_cache,
-                                       k_scale_cache, v_scale_cache,
-                                       slot_mapping, slot_dtype, num_tokens,
-                                       num_kv_heads, num_slots, s)
-          : mskv::launch_store<_Float16>(key, value, k_cache, v_cache,
-                                         k_scale_cache, v_scale_cache,
-                                         slot_mapping, slot_dtype, num_tokens,
-                                         num_kv_heads, num_slots, s);
+  hipError_t e;
+  if (act_dtype == MSKV_BFLOAT16)
+    e = mskv::launch_store<__bf16>(key, value, k_cache, v_cache, k_scale_cache, v_scale_cache,
+                                   slot_mapping, slot_dtype, num_tokens, num_kv_heads,
+                                   num_slots, s);
+  else if (act_dtype == MSKV_FLOAT16)
+    e = mskv::launch_store<_Float16>(key, value, k_cache, v_cache, k_scale_cache,
+                                     v_scale_cache, slot_mapping, slot_dtype, num_tokens,
+                                     num_kv_heads, num_slots, s);
+  else
+    e = mskv::launch_store<float>(key, value, k_cache, v_cache, k_scale_cache, v_scale_cache,
+                                  slot_mapping, slot_dtype, num_tokens, num_kv_heads,
+                                  num_slots, s);
   return (int)e;
 }

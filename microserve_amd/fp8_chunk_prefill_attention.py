@@ -35,7 +35,11 @@ def fp8_chunk_prefill_attention(
     positions read through the flattened ``block_table``
     (``fp8_chunk_prefill_attention.py:70-109``); query ``i`` sees positions
     ``< prefix_len + i + 1``.  ``block_m``/``block_n`` are accepted and
-    ignored.  QK^T and PV run as FP8 MFMA contractions.
+    ignored.  QK^T runs as FP8 MFMA contractions (the query split into exact
+    e4m3 parts, the K bytes as stored); PV runs on the fp16 MFMA, with V's
+    bytes converted to fp16 exactly and fp16 probability weights, which at
+    the same matrix-core time as two FP8 parts of P keeps 11 significant
+    bits for every weight.
     """
     del block_m, block_n
     query = query.contiguous()

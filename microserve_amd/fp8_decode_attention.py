@@ -9,24 +9,29 @@ import torch
 from microserve_amd import _lib
 
 
-# Per device, the split-partials scratch, grown on demand and reused by
-# every call: decode calls on one stream (graph replays included) run one
-# after another, so they never hold it at the same time.  A graph captured
-# before the scratch grew still addresses the old buffer, so a grown-out
-# buffer is retired, never freed; growth at least doubles, so few exist.
+# Per (device, stream), the split-partials scratch, grown on demand and
+# reused by every call on that stream: calls on one stream (graph replays
+# included) run one after another, so they never hold it at the same time,
+# and calls on different streams each have their own, like the reference's
+# call, which keeps no state between calls (fp8_decode_attention.py:93).
+# The buffer is allocated on the stream that uses it (the caching allocator
+# ties a block to the stream it was allocated on).  A graph captured before
+# the scratch grew still addresses the old buffer, so a grown-out buffer is
+# retired, never freed; growth at least doubles, so few exist.
 _SCRATCH: dict = {}
 _RETIRED: list = []
 
 
-def _scratch(device: torch.device, nbytes: int) -> torch.Tensor:
-    buf = _SCRATCH.get(device)
+def _scratch(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    key = (device, stream)
+    buf = _SCRATCH.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(nbytes, 1 << 16)
         if buf is not None:
             _RETIRED.append(buf)
             size = max(size, 2 * buf.numel())
         buf = torch.empty(size, dtype=torch.uint8, device=device)
-        _SCRATCH[device] = buf
+        _SCRATCH[key] = buf
     return buf
 
 
@@ -68,9 +73,9 @@ def fp8_decode_attention(
     (``fp8_decode_attention.py:62-101``), except that ``query`` may be fp16 or
     bf16 and ``block_n`` is accepted and ignored (the tile size is the
     kernel's).  The split-KV partition count depends only on shapes and the
-    partials scratch is a persistent per-device buffer, so the call can be
-    captured in a HIP graph (calls on concurrent streams need their own
-    scratch and are not supported).
+    partials scratch is a persistent buffer per (device, stream), so the call
+    can be captured in a HIP graph, and calls on different streams may run
+    concurrently.
     ``out``, when given, receives the result instead of a new tensor.
     """
     del block_n
@@ -100,7 +105,8 @@ def fp8_decode_attention(
     lib = _lib.load()
     splits, ws_bytes = _plan(batch_size, num_q_heads, num_kv_heads, head_dim,
                              max_num_blocks, block_size)
-    ws = _scratch(query.device, ws_bytes) if ws_bytes else None
+    stream = _lib.stream_of(query)
+    ws = _scratch(query.device, stream, ws_bytes) if ws_bytes else None
     status = lib.mskv_fp8_decode_attention(
         query.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
         k_scale_cache.data_ptr(), v_scale_cache.data_ptr(),
@@ -108,7 +114,6 @@ def fp8_decode_attention(
         batch_size, num_q_heads, num_kv_heads, head_dim, block_size,
         k_cache.shape[0], max_num_blocks, float(softmax_scale),
         _lib.act_dtype(query), splits,
-        ws.data_ptr() if ws is not None else None, ws_bytes,
-        _lib.stream_of(query))
+        ws.data_ptr() if ws is not None else None, ws_bytes, stream)
     _lib.check(status, "fp8_decode_attention")
     return out

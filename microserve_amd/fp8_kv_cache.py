@@ -21,8 +21,9 @@ def store_fp8_kvcache(
     (``fp8_kv_cache.py:42-61``): per (token, kv head) the scale is
     ``max(amax, 1e-8) / 448`` and the bytes are
     ``e4m3fn(clamp(x / scale, -448, 448))``; token ``t`` lands at cache row
-    ``slot_mapping[t]``.  ``key``/``value`` may be fp16 or bf16 (the reference
-    upcasts any float); ``slot_mapping`` may be int32 or int64.
+    ``slot_mapping[t]``.  ``key``/``value`` may be fp16, bf16 or fp32 (the
+    reference upcasts any float to fp32, ``:22-23``); ``slot_mapping`` may be
+    int32 or int64.
     """
     key = key.contiguous()
     value = value.contiguous()
@@ -49,6 +50,6 @@ def store_fp8_kvcache(
         v_cache.data_ptr(), k_scale_cache.data_ptr(), v_scale_cache.data_ptr(),
         slot_mapping.data_ptr(),
         _lib.INT64 if slot_mapping.dtype == torch.int64 else _lib.INT32,
-        num_tokens, num_kv_heads, head_dim, num_slots, _lib.act_dtype(key),
+        num_tokens, num_kv_heads, head_dim, num_slots, _lib.store_dtype(key),
         _lib.stream_of(key))
     _lib.check(status, "store_fp8_kvcache")

@@ -74,8 +74,15 @@ def test_argument_validation_without_launch():
     args = [1] * 8
     assert lib.mskv_fp8_decode_attention(*args, 2, 30, 8, 128, 256, 10, 4, 0.1, 1, 1, None, 0, None) == EINVAL
     assert lib.mskv_fp8_decode_attention(*args, 2, 32, 8, 128, 48, 10, 4, 0.1, 1, 1, None, 0, None) == EUNSUP
-    # decode: GQA group of 24 is neither <= 16 nor a multiple of 16
-    assert lib.mskv_fp8_decode_attention(*args, 2, 48, 2, 128, 256, 10, 4, 0.1, 1, 1, None, 0, None) == EUNSUP
+    # decode: any GQA divisor is accepted (group 24: the last 16-head unit of
+    # each kv head is partly idle); with the right split count the call gets
+    # past the shape checks to the workspace check
+    s24 = lib.mskv_decode_num_splits(2, 48, 2, 4, 256)
+    assert s24 > 1
+    assert lib.mskv_fp8_decode_attention(*args, 2, 48, 2, 128, 256, 10, 4, 0.1, 1, s24, None, 0, None) == EWS
+    # store: fp32 key/value rows are accepted (zero tokens: a no-op)
+    assert lib.mskv_store_fp8_kvcache(None, None, None, None, None, None, None, 1, 0, 8, 128, 100, _lib.FLOAT32, None) == 0
+    assert lib.mskv_store_fp8_kvcache(1, 1, 1, 1, 1, 1, 1, 1, 4, 8, 128, 100, 3, None) == EINVAL
     # decode: wrong split count, missing workspace
     s = lib.mskv_decode_num_splits(2, 32, 8, 4, 256)
     assert lib.mskv_fp8_decode_attention(*args, 2, 32, 8, 128, 256, 10, 4, 0.1, 1, s + 1, None, 0, None) == EINVAL

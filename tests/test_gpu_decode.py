@@ -73,7 +73,8 @@ def test_decode_qwen3_06b_config(dtype):
     _run_and_check(query, lens, tables, caches)
 
 
-@pytest.mark.parametrize("hq,hk", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1), (32, 2), (64, 2)])
+@pytest.mark.parametrize("hq,hk", [(8, 8), (16, 8), (32, 8), (64, 8), (16, 1), (32, 2), (64, 2),
+                                   (24, 8), (40, 2), (20, 1), (96, 4)])
 def test_decode_gqa_groups(hq, hk):
     lens = [1, 255, 256, 257, 700, 0, 1023, 33]
     query, tables, caches = _setup(41 + hq + hk, lens, hq, hk, 40)
@@ -112,6 +113,30 @@ def test_decode_invalid_block_ids_read_as_empty():
     ref1 = O.decode_attention(query[1:], kc, vc, ks, vs, torch.tensor([512]), tables[1:], H.D ** -0.5)
     H.assert_attention_close(out[:1], ref0)
     H.assert_attention_close(out[1:], ref1)
+
+
+def test_decode_invalid_first_page_keeps_weight_precision():
+    """A split whose first page is an invalid block id sees no valid token
+    in its first steps.  The PV weights' power-of-two scale is then chosen at
+    the first step that has one, so V rows with small scales (V ~ 1e-4,
+    v_scale ~ 1e-6) keep fp16's 11 significant bits instead of going
+    subnormal.  At batch 64 x 4096 a split holds four pages, so sequence 0's
+    first split still has three valid pages after its invalid first one; its
+    result is attention over pages 1-15."""
+    lens = [4096] * 64
+    assert decode_num_splits(64, 32, 8, 16, H.BLOCK) == 4
+    query, tables, caches = _setup(73, lens, 32, 8, 1100, vscale=1e-4)
+    bad = tables.clone()
+    bad[0, 0] = 1 << 20
+    out = fp8_decode_attention(query.to(H.DEV), *caches,
+                               torch.tensor(lens, dtype=torch.int32, device=H.DEV),
+                               bad.to(H.DEV), H.D ** -0.5)
+    torch.cuda.synchronize()
+    kc, vc, ks, vs = H.cache_to_numpy(*caches)
+    ref = O.decode_attention(query[:1], kc, vc, ks, vs, torch.tensor([4096 - H.BLOCK]),
+                             tables[:1, 1:].contiguous(), H.D ** -0.5)
+    max_abs, rel = H.attention_errors(out[:1], ref)
+    assert rel < 2e-3, f"max_abs {max_abs:.3e} rel {rel:.3e}"
 
 
 @pytest.mark.parametrize("block_size", [512, 1024])
@@ -383,10 +408,12 @@ def test_decode_scratch_reuse_across_shapes():
 
 
 def test_decode_graph_survives_scratch_growth(monkeypatch):
-    """A graph captured before a larger batch grew the partials scratch still
-    replays correctly: the buffer it addresses is kept, not handed back to
-    the allocator for other tensors (the runner captures its graphs from the
-    smallest batch up, with an eager warm-up of each before capture)."""
+    """A graph captured before a larger batch grew its stream's partials
+    scratch still replays correctly: the buffer it addresses is kept, not
+    handed back to the allocator for other tensors (the runner captures its
+    graphs from the smallest batch up, with an eager warm-up of each before
+    capture).  The scratch is per (device, stream): here the warm-up, the
+    capture and the growth all run on one capture stream."""
     M = importlib.import_module("microserve_amd.fp8_decode_attention")
     monkeypatch.setattr(M, "_SCRATCH", {})
     monkeypatch.setattr(M, "_RETIRED", [])
@@ -408,13 +435,18 @@ def test_decode_graph_survives_scratch_growth(monkeypatch):
         step()
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    captured = M._SCRATCH[q.device]
+    key = (q.device, s.cuda_stream)
+    captured = M._SCRATCH[key]
     graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
+    with torch.cuda.graph(graph, stream=s):
         step()
-    want = fp8_decode_attention(q, *caches, lens_d, t, 0.088)
+    assert M._SCRATCH[key] is captured, "the capture must reuse the warmed-up scratch"
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        want = fp8_decode_attention(q, *caches, lens_d, t, 0.088)
+    torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
-    assert M._SCRATCH[q.device] is not captured, "the large batch must grow the scratch"
+    assert M._SCRATCH[key] is not captured, "the large batch must grow the scratch"
     assert any(r is captured for r in M._RETIRED)
     # tensors of the old buffer's size, filled with a pattern: a freed
     # buffer would be handed to one of them and the replay would overwrite it
@@ -429,3 +461,35 @@ def test_decode_graph_survives_scratch_growth(monkeypatch):
     assert (got.float() - want[:1].float()).abs().max().item() < 1e-2
     for c in churn:
         assert bool((c == 0x5A).all()), "the replay wrote into another tensor"
+
+
+def test_decode_concurrent_streams_match_the_oracle():
+    """Two streams decode different batches at the same time: each stream has
+    its own partials scratch, so neither overwrites the other's, as with the
+    reference, whose call keeps no state between calls
+    (``fp8_decode_attention.py:93``).  Both batches use several splits."""
+    lens_a = [4096] * 16
+    lens_b = [3000 + 37 * i for i in range(16)]
+    qa, ta, caches = _setup(151, lens_a + lens_b, 32, 8, 1100)
+    qb, tb = qa[16:].contiguous(), ta[16:].contiguous()
+    qa, ta = qa[:16].contiguous(), ta[:16].contiguous()
+    assert decode_num_splits(16, 32, 8, ta.shape[1], H.BLOCK) > 1
+    args_a = (qa.to(H.DEV), ta.to(H.DEV), torch.tensor(lens_a, dtype=torch.int32, device=H.DEV))
+    args_b = (qb.to(H.DEV), tb.to(H.DEV), torch.tensor(lens_b, dtype=torch.int32, device=H.DEV))
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    s1.wait_stream(torch.cuda.current_stream())
+    s2.wait_stream(torch.cuda.current_stream())
+    outs_a, outs_b = [], []
+    for _ in range(4):
+        with torch.cuda.stream(s1):
+            outs_a.append(fp8_decode_attention(args_a[0], *caches, args_a[2], args_a[1], 0.088))
+        with torch.cuda.stream(s2):
+            outs_b.append(fp8_decode_attention(args_b[0], *caches, args_b[2], args_b[1], 0.088))
+    torch.cuda.synchronize()
+    kc, vc, ks, vs = H.cache_to_numpy(*caches)
+    ref_a = O.decode_attention(qa, kc, vc, ks, vs, torch.tensor(lens_a), ta, 0.088)
+    ref_b = O.decode_attention(qb, kc, vc, ks, vs, torch.tensor(lens_b), tb, 0.088)
+    for oa, ob in zip(outs_a, outs_b):
+        H.assert_attention_close(oa, ref_a)
+        H.assert_attention_close(ob, ref_b)
+        assert torch.equal(oa, outs_a[0]) and torch.equal(ob, outs_b[0])

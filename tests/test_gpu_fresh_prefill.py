@@ -68,7 +68,8 @@ def test_fresh_prefill_ragged_batch(dtype):
     _check(q, k, v, cu_q, cu_k, lens, lens)
 
 
-@pytest.mark.parametrize("hq,hk", [(16, 8), (8, 8), (64, 8), (32, 2), (16, 1)])
+@pytest.mark.parametrize("hq,hk", [(16, 8), (8, 8), (64, 8), (32, 2), (16, 1), (24, 8), (40, 2),
+                                   (20, 1), (48, 2)])
 def test_fresh_prefill_gqa_groups(hq, hk):
     lens = [70, 129]
     q, k, v, cu_q, cu_k = _setup(411 + hq, lens, lens, hq, hk)

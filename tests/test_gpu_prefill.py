@@ -79,7 +79,8 @@ def test_varlen_prefill_mixed_batch(dtype):
     _varlen_check(query, tables, caches, cu_q, cu_k, lq)
 
 
-@pytest.mark.parametrize("hq,hk", [(16, 8), (8, 8), (64, 8), (32, 2), (16, 1)])
+@pytest.mark.parametrize("hq,hk", [(16, 8), (8, 8), (64, 8), (32, 2), (16, 1), (24, 8), (40, 2),
+                                   (20, 1), (48, 2)])
 def test_varlen_prefill_gqa_groups(hq, hk):
     lq = [64, 130]
     lk = [64 + 300, 130 + 5]
@@ -182,11 +183,13 @@ def test_varlen_prefill_v_scale_ratio_inside_a_tile(r, dtype):
     """The reference dequantizes V per element
     (fp8_chunk_prefill_attention.py:49-50,60), so a key with a huge V in the
     same tile costs the other keys nothing.  The PV product here weights
-    each key by fp16(p * v_scale * fw), fw set from the largest v_scale the
-    wave has seen; fp16's exponent range keeps the dominant keys' weights at
-    11 significant bits whatever that ratio.  The error must stay at its
-    ratio-1 level (measured rel 1.66e-3 bf16, 2.8e-4 fp16 at every ratio up
-    to 10000; fp16 inputs overflow beyond that), far inside the usual gate."""
+    each key by fp16(p) * fp16(v_scale * fw), fw set from the largest v_scale
+    the wave has seen: a key whose v_scale lies within 2^21 of that largest
+    one keeps a normal fp16 scale (11 significant bits), so at every ratio
+    tested here the error must stay at its ratio-1 level (measured rel
+    1.66e-3 bf16, 2.8e-4 fp16 at every ratio up to 10000; fp16 inputs
+    overflow beyond that), far inside the usual gate.  Ratios past 2^21 give
+    the smaller keys subnormal scales with fewer bits (not tested)."""
     query, tables, caches, cu_q, cu_k, lq = _v_ratio_case(r, dtype)
     max_abs, rel = _varlen_check(query, tables, caches, cu_q, cu_k, lq)
     print(f"V-scale ratio {r} {dtype}: max_abs {max_abs:.4e} rel {rel:.4e}")

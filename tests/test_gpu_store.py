@@ -64,6 +64,31 @@ def test_store_matches_oracle_bytes(dtype, slot_dtype):
             assert bad.size == 0, f"{name}: {len(bad)} mismatched bytes, first {bad[:3]}"
 
 
+def test_store_fp32_rows_match_oracle_bytes():
+    """fp32 K/V rows (the reference upcasts any float input,
+    ``fp8_kv_cache.py:22-23``): full 24-bit mantissas exercise the division
+    far beyond the 8 and 11 bits of bf16 and fp16 rows, plus the edge rows
+    (zeros, -0, outliers, amax 448, fp32 subnormals, 1e30)."""
+    gen = torch.Generator().manual_seed(17)
+    nb, n = 32, 7000
+    key = torch.randn(n, 8, H.D, generator=gen) * torch.exp(
+        torch.randn(n, 8, 1, generator=gen) * 4)
+    key[:4] = _edge_rows(torch.float32, gen, 4)
+    value = torch.randn(n, 8, H.D, generator=gen)
+    value[-4:] = _edge_rows(torch.float32, gen, 4)
+    slots = torch.randperm(nb * H.BLOCK, generator=gen)[:n]
+    kc, vc, ks, vs = H.alloc_cache(nb)
+    store_fp8_kvcache(key.to(H.DEV), value.to(H.DEV), kc, vc, ks, vs, slots.to(H.DEV))
+    got = H.cache_to_numpy(kc, vc, ks, vs)
+    want = H.oracle_store_numpy(key, value, slots, nb)
+    for g, w, name in zip(got, want, ("k_cache", "v_cache", "k_scale", "v_scale")):
+        if g.dtype == np.float32:
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32)), name
+        else:
+            bad = np.argwhere(g != w)
+            assert bad.size == 0, f"{name}: {len(bad)} mismatched bytes, first {bad[:3]}"
+
+
 def test_store_division_sensitive_rows():
     with open(os.path.join(GOLDEN, "division_rows.json")) as f:
         rows = json.load(f)

@@ -3,8 +3,10 @@ that allocates nothing (its split partials live in a library-owned device
 array): called through the C ABI, its output equals mskv_fp8_decode_attention's
 bit for bit on two calls in a row, the second with a smaller input (the array
 then holds the first call's partials), then on a ragged batch whose grid runs
-the longest-first work items (kept in the same array); a shape whose
-partials exceed the array is rejected."""
+the longest-first work items (kept in the same array); captured in a HIP
+graph after an eager warm-up, its replays with new lengths equal the
+workspace entry point's eager output; a shape whose partials exceed the
+array is rejected."""
 
 import numpy as np
 
@@ -93,6 +95,44 @@ def test_noalloc_decode_work_items_in_the_array():
         want = fp8_decode_attention(q, *caches, seqlens, tables, scale)
         torch.cuda.synchronize()
         assert torch.equal(out, want), f"call {it}"
+
+
+def test_noalloc_decode_under_graph_capture():
+    """After one eager call on the device (which looks up the array's address
+    there), the call is captured into a HIP graph on the work-item shape (48
+    ragged sequences, 17 splits) and replayed three times with new lengths,
+    eager work and synchronizations between the replays: every replay equals
+    the workspace entry point's eager output bit for bit."""
+    scale = H.D ** -0.5
+    gen = torch.Generator().manual_seed(305)
+    b = 48
+    lens = torch.exp(torch.empty(b).uniform_(np.log(16), np.log(32768), generator=gen)).long().tolist()
+    lens[0] = 32768
+    pages = sum((n + H.BLOCK - 1) // H.BLOCK for n in lens)
+    q, caches, seqlens, tables = _setup(306, lens, 32, 8, pages + 9)
+    assert b * decode_num_splits(b, 32, 8, tables.shape[1], H.BLOCK) > 512
+    out = torch.empty_like(q)
+    assert _noalloc(q, caches, seqlens, tables, out, scale) == 0
+    torch.cuda.synchronize()
+    static_lens = seqlens.clone()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.graph(graph, stream=s):
+        status = _noalloc(q, caches, static_lens, tables, out, scale)
+    assert status == 0
+    torch.cuda.synchronize()
+    for it in range(3):
+        new = [max(0, n - (it + 1) * n // 5) for n in lens]
+        new[it] = 0
+        static_lens.copy_(torch.tensor(new, dtype=torch.int32))
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        want = fp8_decode_attention(q, *caches, static_lens, tables, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {it}"
 
 
 def test_noalloc_decode_rejects_partials_over_the_limit():
