@@ -451,28 +451,44 @@ void decode_fp8_kernel(DecodeArgs a) {
 // o_s over those splits, for four consecutive d.  m = -inf (den = 0, o = 0)
 // holds no split.
 //
-// Folds the splits sp = first + k * stride (k < K, sp < nvalid) of one row
-// into (m, den, o): every lse value and partial quad is loaded before any
-// is used, so the K splits cost one memory round trip.  Partials past
-// nvalid are never read.
+// The lse values and partial quads of splits sp = first + k * stride
+// (k < K), loaded all at once (one memory round trip) for sp < limit; the
+// rest read as empty.
 template <int K>
-__device__ __forceinline__ void merge_splits(float& m, float& den, f32x4& o,
-                                             const float* __restrict__ lse,
-                                             const float* __restrict__ po, int first,
-                                             int stride, int nvalid) {
+struct SplitLoads {
   float ls[K];
   f32x4 pv[K];
+};
+template <int K>
+__device__ __forceinline__ void load_splits(SplitLoads<K>& s, const float* __restrict__ lse,
+                                            const float* __restrict__ po, int first, int stride,
+                                            int limit) {
 #pragma unroll
   for (int k = 0; k < K; ++k) {
     const int sp = first + k * stride;
-    const bool ok = sp < nvalid;
-    ls[k] = ok ? lse[sp] : -INFINITY;
-    pv[k] = ok ? *reinterpret_cast<const f32x4*>(po + (int64_t)sp * kHeadDim)
-               : f32x4{0.f, 0.f, 0.f, 0.f};
+    const bool ok = sp < limit;
+    s.ls[k] = ok ? lse[sp] : -INFINITY;
+    s.pv[k] = ok ? *reinterpret_cast<const f32x4*>(po + (int64_t)sp * kHeadDim)
+                 : f32x4{0.f, 0.f, 0.f, 0.f};
   }
-  float cm = ls[0];
+}
+
+// Folds the loaded splits below nvalid into (m, den, o).  Loads past nvalid
+// (stale partials of an earlier call, when the caller loaded up to the
+// split count) are dropped, values included.
+template <int K>
+__device__ __forceinline__ void fold_splits(float& m, float& den, f32x4& o, SplitLoads<K> s,
+                                            int first, int stride, int nvalid) {
 #pragma unroll
-  for (int k = 1; k < K; ++k) cm = fmaxf(cm, ls[k]);
+  for (int k = 0; k < K; ++k) {
+    if (first + k * stride >= nvalid) {
+      s.ls[k] = -INFINITY;
+      s.pv[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  float cm = s.ls[0];
+#pragma unroll
+  for (int k = 1; k < K; ++k) cm = fmaxf(cm, s.ls[k]);
   const float nm = fmaxf(m, cm);
   if (nm == -INFINITY) return;  // no split here, none before
   const float sc = m == -INFINITY ? 0.0f : exp2_fast(m - nm);
@@ -480,11 +496,24 @@ __device__ __forceinline__ void merge_splits(float& m, float& den, f32x4& o,
   o *= sc;
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    const float w = exp2_fast(ls[k] - nm);  // 0 for a split not read
+    const float w = exp2_fast(s.ls[k] - nm);  // 0 for a split not read
     den += w;
-    o += w * pv[k];
+    o += w * s.pv[k];
   }
   m = nm;
+}
+
+// Folds the splits sp = first + k * stride (k < K, sp < nvalid) of one row
+// into (m, den, o) in one memory round trip.  Partials past nvalid are
+// never read.
+template <int K>
+__device__ __forceinline__ void merge_splits(float& m, float& den, f32x4& o,
+                                             const float* __restrict__ lse,
+                                             const float* __restrict__ po, int first,
+                                             int stride, int nvalid) {
+  SplitLoads<K> s;
+  load_splits(s, lse, po, first, stride, nvalid);
+  fold_splits(m, den, o, s, first, stride, nvalid);
 }
 
 // (m, den, o) becomes the merge of states a and b over disjoint splits.
@@ -645,15 +674,22 @@ __global__ __launch_bounds__(64 * kWideWaves) void decode_combine_wide_kernel(
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int i = lane & 7, j = lane >> 3;
-  const int L = min(seqlens[b], max_tokens);
-  const int nvalid = L <= 0 ? 0 : min(splits, (L + split_tokens - 1) / split_tokens);
-  if (nvalid == 1) return;  // written by the split kernel
   const int d = 32 * quarter + 4 * i;
   const float* lse = part_lse + (int64_t)row * splits;
   const float* po = part_o + (int64_t)row * splits * kHeadDim + d;
+  // the first kWideK splits of each lane are loaded (every split row below
+  // `splits` is in bounds) while the sequence length is still on its way:
+  // one memory round trip for up to 256 splits instead of two
+  constexpr int kPass = 8 * kWideWaves * kWideK;
+  SplitLoads<kWideK> first;
+  load_splits(first, lse, po, 8 * wave + j, 8 * kWideWaves, min(splits, kPass));
+  const int L = min(seqlens[b], max_tokens);
+  const int nvalid = L <= 0 ? 0 : min(splits, (L + split_tokens - 1) / split_tokens);
+  if (nvalid == 1) return;  // written by the split kernel
   float m = -INFINITY, den = 0.0f;
   f32x4 o = {0.f, 0.f, 0.f, 0.f};
-  for (int base = 0; base < nvalid; base += 8 * kWideWaves * kWideK)
+  fold_splits(m, den, o, first, 8 * wave + j, 8 * kWideWaves, nvalid);
+  for (int base = kPass; base < nvalid; base += kPass)
     merge_splits<kWideK>(m, den, o, lse, po, base + 8 * wave + j, 8 * kWideWaves, nvalid);
   {
     const f32x4 ox = {__shfl_xor(o[0], 8), __shfl_xor(o[1], 8), __shfl_xor(o[2], 8),
