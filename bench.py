@@ -143,24 +143,28 @@ def cpu_baseline(w, budget_s=10.0):
         t_total += time.perf_counter() - t0
         done += 1
     gbs = decode_bytes(done, CTX, HQ, HK, D) / t_total / 1e9
-    # the store on the host: the oracle quantizing and scattering a bounded
-    # sample of the fill's tokens (the first 16,384 of them)
-    key, value, slots = (t[:16384].cpu() for t in w["fills"][0])
-    skc = np.zeros(tuple(w["kc"].shape), np.uint8)
-    svc = np.zeros_like(skc)
-    sks = np.ones(tuple(w["ks"].shape), np.float32)
-    svs = np.ones_like(sks)
-    t0 = time.perf_counter()
-    O.store_fp8_kvcache(key.float().numpy(), value.float().numpy(), skc, svc, sks, svs,
-                        slots.numpy())
-    store_s = time.perf_counter() - t0
+    # the store on the host: the oracle's store vectorized in torch CPU ops
+    # (torch's intra-op threads on every core) over a bounded sample of the
+    # fill's tokens (the first 65,536 of them), best of three passes
+    key, value, slots = (t[:65536].cpu() for t in w["fills"][0])
+    skc = torch.zeros(tuple(w["kc"].shape), dtype=torch.uint8)
+    svc = torch.zeros_like(skc)
+    sks = torch.ones(tuple(w["ks"].shape))
+    svs = torch.ones_like(sks)
+    store_s = float("inf")
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.store_fp8_kvcache_torch(key, value, skc, svc, sks, svs, slots)
+        store_s = min(store_s, time.perf_counter() - t0)
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": torch.get_num_threads(),
             "os_cpu_count": os.cpu_count(), "kind": "port",
             "sample": f"{done} single-sequence decodes (4096 tokens, 32 q / 8 kv heads) "
                       f"cycling over the Qwen3-8B batch, torch fp32 oracle, {t_total:.1f} s",
             "store": {"value": round(key.shape[0] / store_s, 1), "unit": "tokens/s",
-                      "sample": f"{key.shape[0]} tokens of the 262,144-token fill, numpy "
-                                f"oracle, {store_s:.2f} s"}}
+                      "cores": torch.get_num_threads(), "kind": "port",
+                      "sample": f"{key.shape[0]} tokens of the 262,144-token fill, the oracle's "
+                                f"store vectorized in torch CPU ops, best of 3 passes, "
+                                f"{store_s:.2f} s"}}
 
 
 C1_HQ, C1_BATCH, C1_POOL, C1_MAXLEN = 16, 4, 64, 1024
@@ -230,16 +234,16 @@ def time_config1(dev, iters=200, warmup=20, cpu_budget_s=8.0, cpu=True):
         return res
     from oracle import fp8_oracle as O
     torch.set_num_threads(os.cpu_count() or 1)
-    kc = np.zeros((C1_POOL, BS, HK, D), np.uint8)
-    vc = np.zeros_like(kc)
-    ks = np.ones((C1_POOL, BS, HK), np.float32)
-    vs = np.ones_like(ks)
-    kf, vf, sl = w["key"].float().numpy(), w["value"].float().numpy(), w["slots"].numpy()
+    kc = torch.zeros(C1_POOL, BS, HK, D, dtype=torch.uint8)
+    vc = torch.zeros_like(kc)
+    ks = torch.ones(C1_POOL, BS, HK)
+    vs = torch.ones_like(ks)
+    kf, vf, sl = w["key"], w["value"], w["slots"]
     t_store = t_dec = 0.0
     reps = 0
     while t_store + t_dec < cpu_budget_s:
         t0 = time.perf_counter()
-        O.store_fp8_kvcache(kf, vf, kc, vc, ks, vs, sl)
+        O.store_fp8_kvcache_torch(kf, vf, kc, vc, ks, vs, sl)
         t1 = time.perf_counter()
         O.decode_attention(w["q"], kc, vc, ks, vs, w["lens"], w["tables"], D ** -0.5)
         t2 = time.perf_counter()
@@ -248,13 +252,13 @@ def time_config1(dev, iters=200, warmup=20, cpu_budget_s=8.0, cpu=True):
         reps += 1
     res["cpu_baseline"] = {
         "store_tokens_per_s": round(reps * n / t_store, 1),
-        "store_cores": 1,
+        "store_cores": torch.get_num_threads(),
         "decode_gbs": round(reps * dec_bytes / t_dec / 1e9, 3),
         "decode_cores": torch.get_num_threads(),
         "step_us": round((t_store + t_dec) / reps * 1e6, 1),
         "kind": "port",
-        "sample": f"{reps} repetitions of the whole step: numpy store oracle (one core), "
-                  f"torch fp32 decode oracle, {t_store + t_dec:.1f} s"}
+        "sample": f"{reps} repetitions of the whole step: the oracle's store vectorized in "
+                  f"torch CPU ops and its torch fp32 decode, {t_store + t_dec:.1f} s"}
     return res
 
 
@@ -334,12 +338,14 @@ def time_prefill(dev, iters=20, warmup=40, dtype=torch.bfloat16):
     us, us_cold = _time_sustained(lambda: run_prefill(w), iters, warmup)
     flop = prefill_flops(PRE_SEQS, PRE_CACHED, PRE_NEW, HQ, D)
     tflops = flop / us / 1e6
-    return {"workload": "varlen chunked prefill, 8 seqs x (8192 cached + 2048 new), "
-                        f"32 q / 8 kv heads, fp8 cache, {str(dtype).split('.')[-1]} q",
-            "us": round(us, 2), "flop": flop, "tflops": round(tflops, 1),
-            "peak_tflops": FP8_PEAK_TFLOPS, "frac": round(tflops / FP8_PEAK_TFLOPS, 4),
-            "timing": f"mean of calls {warmup + 1}-{warmup + iters} after a 1 s idle",
-            "us_first_calls": round(us_cold, 2)}
+    dname = "bf16" if dtype == torch.bfloat16 else "fp16"
+    return _with_mfma({
+        "workload": "varlen chunked prefill, 8 seqs x (8192 cached + 2048 new), "
+                    f"32 q / 8 kv heads, fp8 cache, {str(dtype).split('.')[-1]} q",
+        "us": round(us, 2), "flop": flop, "tflops": round(tflops, 1),
+        "peak_tflops": FP8_PEAK_TFLOPS, "frac": round(tflops / FP8_PEAK_TFLOPS, 4),
+        "timing": f"mean of calls {warmup + 1}-{warmup + iters} after a 1 s idle",
+        "us_first_calls": round(us_cold, 2)}, f"prefill_fp8_{dname}")
 
 
 _SPIN_CYCLES_PER_MS = None
@@ -551,12 +557,13 @@ def time_fresh_prefill(dev, iters=20, warmup=30, dtype=torch.bfloat16):
     flop = prefill_flops(FRESH_SEQS, 0, FRESH_LEN, HQ, D)
     tflops = flop / us / 1e6
     dname = "bf16" if dtype == torch.bfloat16 else "fp16"
-    return {"workload": "fresh causal prefill, 8 seqs x 8192 tokens, 32 q / 8 kv heads, "
-                        f"{dname} q/k/v (16-bit MFMA)",
-            "us": round(us, 2), "flop": flop, "tflops": round(tflops, 1),
-            "peak_tflops": BF16_PEAK_TFLOPS, "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
-            "timing": f"mean of calls {warmup + 1}-{warmup + iters} after a 1 s idle",
-            "us_first_calls": round(us_cold, 2)}
+    return _with_mfma({
+        "workload": "fresh causal prefill, 8 seqs x 8192 tokens, 32 q / 8 kv heads, "
+                    f"{dname} q/k/v (16-bit MFMA)",
+        "us": round(us, 2), "flop": flop, "tflops": round(tflops, 1),
+        "peak_tflops": BF16_PEAK_TFLOPS, "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+        "timing": f"mean of calls {warmup + 1}-{warmup + iters} after a 1 s idle",
+        "us_first_calls": round(us_cold, 2)}, f"dense_prefill_{dname}")
 
 
 class _Seq:
@@ -778,20 +785,17 @@ def time_norm_rope(dev, iters=20, warmup=3):
 
         res = {}
         for name, fn in (("fused", fused), ("unfused", unfused)):
-            # back-to-back calls between two events: the device time per call
-            # when the GPU outruns the host (the large step), the per-call
-            # host cost when it does not (the 64-token step)
-            for _ in range(warmup):
-                fn()
-            torch.cuda.synchronize()
-            stream = torch.cuda.current_stream()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record(stream)
-            for _ in range(iters):
-                fn()
-            e1.record(stream)
-            torch.cuda.synchronize()
-            res[name] = e0.elapsed_time(e1) / iters * 1e3
+            # device time per call: the calls queued behind a spin kernel
+            # (_time_steps), so no host launch time is counted
+            res[name] = _time_steps(lambda i: fn(), iters, warmup)
+        # the host's cost per fused call (ctypes and Python argument checks):
+        # back-to-back calls with no spin ahead, wall clock per call
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fused()
+        host_us = (time.perf_counter() - t0) / iters * 1e6
+        torch.cuda.synchronize()
         nbytes = norm_rope_bytes(n, HQ, HK, with_k)
         cpu = (_cpu_norm_rope(qkv, pos, qw, kw, cos_t, sin_t, slots, nb)
                if mode == "prefill" and dt == torch.bfloat16 else None)
@@ -800,6 +804,7 @@ def time_norm_rope(dev, iters=20, warmup=3):
                                 f"40960 x 128",
                     "us": round(res["fused"], 2), "unfused_us": round(res["unfused"], 2),
                     "speedup": round(res["unfused"] / res["fused"], 2),
+                    "host_us_per_call": round(host_us, 2),
                     "bytes": nbytes, "gbs": round(nbytes / res["fused"] / 1e3, 1),
                     "frac": round(nbytes / res["fused"] / 1e3 / HBM_PEAK_GBS, 4),
                     **({"cpu_baseline": cpu} if cpu else {})})
@@ -823,9 +828,11 @@ def _cpu_norm_rope(qkv, pos, qw, kw, cos_t, sin_t, slots, nb, sample=4096):
     vc = np.zeros_like(kc)
     ks = np.ones((nb, BS, HK), np.float32)
     vs = np.ones_like(ks)
+    kc, vc = torch.from_numpy(kc), torch.from_numpy(vc)
+    ks, vs = torch.from_numpy(ks), torch.from_numpy(vs)
     t0 = time.perf_counter()
     _, rk = NR.qk_norm_rope(q, k, p, w_q, w_k, 1e-6, c, s_)
-    O.store_fp8_kvcache(rk.float().numpy(), v.float().numpy(), kc, vc, ks, vs, sl)
+    O.store_fp8_kvcache_torch(rk, v, kc, vc, ks, vs, torch.from_numpy(sl))
     dt = time.perf_counter() - t0
     return {"value": round(sample / dt, 1), "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port", "sample": f"{sample} tokens of the prefill step, oracle in numpy/torch "
@@ -852,6 +859,36 @@ def calibrate_copy(dev, nbytes=1 << 30, iters=5):
     torch.cuda.synchronize()
     print(json.dumps({"calibration": "torch copy_", "bytes_read_per_launch": nbytes,
                       "bytes_written_per_launch": nbytes, "launches": iters}), flush=True)
+
+
+def mfma_counters(name):
+    """MFMA utilization of a prefill kernel from the committed rocprofv3
+    --pmc summary: the busy fraction of the matrix pipe
+    (SQ_VALU_MFMA_BUSY_CYCLES over the SIMDs' active cycles) and VALU
+    instructions per MFMA.  frac / mfma_busy is the fraction of peak the
+    kernel's own instruction mix would reach with the pipe always busy."""
+    path = os.path.join(ROOT, "profiles", "prefill_kernel_trace_and_mfma.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith(f"mfma_counters {name}:"):
+                    kv = dict(x.split("=") for x in line.split(":", 1)[1].split())
+                    return ({"mfma_busy": float(kv["mfma_busy"]),
+                             "valu_per_mfma": float(kv["valu_per_mfma"]),
+                             "mfma_source": os.path.relpath(path, ROOT)})
+    except (OSError, ValueError, KeyError):
+        pass
+    return {}
+
+
+def _with_mfma(res, name):
+    """res plus the kernel's MFMA counters and the fraction of peak at a
+    fully busy matrix pipe."""
+    c = mfma_counters(name)
+    if c:
+        res.update(c)
+        res["frac_at_full_mfma"] = round(res["frac"] / c["mfma_busy"], 4)
+    return res
 
 
 def measured_traffic():

@@ -24,6 +24,9 @@ How each function is pinned (the checks live in ``tests/test_oracle.py``):
   same formula evaluated with torch CPU ops, and by closed forms (a row whose
   amax is 448 has scale exactly 1 and bytes equal to the plain cast; an
   all-zero row has scale 1e-8/448 and bytes 0x00 / 0x80 for -0.0).
+* ``store_fp8_kvcache_torch`` -- the same store vectorized in torch CPU ops
+  (the bench's multi-core baseline).  Pinned against ``store_fp8_kvcache``
+  byte for byte on edge rows and random rows with skipped slots.
 * ``store_fp8_kvcache`` -- placement ``row = (slot // BS) * BS + slot % BS``
   (``fp8_kv_cache.py:29-39``), which equals the fp16 path's
   ``index_copy_`` row (``attention.py:11-21``).  Pinned by brute-force
@@ -166,6 +169,29 @@ def store_fp8_kvcache(key, value, k_cache, v_cache, k_scale_cache,
         vc[r] = vq[t]
         ksc[r] = ks[t]
         vsc[r] = vs[t]
+
+
+def store_fp8_kvcache_torch(key, value, k_cache, v_cache, k_scale_cache,
+                            v_scale_cache, slot_mapping) -> None:
+    """``store_fp8_kvcache`` vectorized in torch CPU ops, for timing on the
+    host's cores (torch's intra-op threads): the reference's formula as its
+    own tests write it (``tests/test_fp8.py:25-26``; ``fp8_kv_cache.py:24-27``)
+    -- ``s = max(amax, 1e-8) / 448``, ``q = e4m3fn(clamp(x / s, -448, 448))``
+    -- and one ``index_copy_`` per cache at rows ``slot``
+    (``attention.py:11-21``).  Same arguments and effect as
+    ``store_fp8_kvcache``, with torch tensors: ``key``/``value`` float
+    ``[N, H_kv, D]``, uint8 byte caches, float32 scale caches, int64 slots.
+    """
+    nb, bs, h, d = k_cache.shape
+    slots = slot_mapping.reshape(-1).to(torch.int64)
+    valid = (slots >= 0) & (slots < nb * bs)
+    rows = slots[valid]
+    for x, cache, scales in ((key, k_cache, k_scale_cache), (value, v_cache, v_scale_cache)):
+        x = x.float()
+        sc = x.abs().amax(-1).clamp_min(_F32_EPS_FLOOR) / _F32_MAX
+        q = (x / sc[..., None]).clamp(-_F32_MAX, _F32_MAX).to(torch.float8_e4m3fn)
+        cache.view(nb * bs, h, d).index_copy_(0, rows, q.view(torch.uint8)[valid])
+        scales.view(nb * bs, h).index_copy_(0, rows, sc[valid])
 
 
 # --------------------------------------------------------------------------

@@ -197,6 +197,44 @@ def test_decode_ragged_fragmented(dtype):
     _run_and_check(query, lens, tables, caches)
 
 
+def test_decode_work_items_cover_every_split_4096_sequences():
+    """The pre-pass at its batch limit: 4096 sequences (the sort's LDS
+    arrays full), mostly one split each plus a few of 16, with the workspace
+    filled with NaN bytes first, so a split that no work item covered would
+    merge a NaN partial.  Called through the C ABI with that workspace."""
+    from microserve_amd import _lib
+    gen = torch.Generator().manual_seed(107)
+    b, w = 4096, 64
+    lens = torch.randint(1, 65, (b,), generator=gen).tolist()
+    for i in range(0, b, 512):
+        lens[i] = w * H.BLOCK
+        lens[i + 1] = 2000
+    lens[3] = 0
+    splits = decode_num_splits(b, 32, 8, w, H.BLOCK)
+    assert splits == 16
+    pages = sum((n + H.BLOCK - 1) // H.BLOCK for n in lens)
+    query, tables, caches = _setup(108, lens, 32, 8, pages + 5)
+    assert tables.shape[1] == w
+    lib = _lib.load()
+    need = lib.mskv_decode_workspace_bytes(b, 32, 8, H.D, splits)
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=H.DEV)
+    q = query.to(H.DEV)
+    out = torch.empty_like(q)
+    kc, vc, ks, vs = caches
+    seqlens = torch.tensor(lens, dtype=torch.int32, device=H.DEV)
+    t = tables.to(H.DEV)
+    status = lib.mskv_fp8_decode_attention(
+        q.data_ptr(), kc.data_ptr(), vc.data_ptr(), ks.data_ptr(), vs.data_ptr(),
+        seqlens.data_ptr(), t.data_ptr(), out.data_ptr(), b, 32, 8, H.D, H.BLOCK, kc.shape[0], w,
+        H.D ** -0.5, _lib.act_dtype(q), splits, ws.data_ptr(), need, _lib.stream_of(q))
+    assert status == 0
+    torch.cuda.synchronize()
+    kcn, vcn, ksn, vsn = H.cache_to_numpy(*caches)
+    ref = O.decode_attention(query, kcn, vcn, ksn, vsn, torch.tensor(lens), tables, H.D ** -0.5)
+    H.assert_attention_close(out, ref)
+    assert (out[3] == 0).all()
+
+
 def test_decode_narrow_workgroups_wide_gqa_group():
     """GQA 32 (64 q / 2 kv heads: two 16-head units per kv head, four in
     all) on the 4-wave workgroup shape over the work items: 96 sequences x

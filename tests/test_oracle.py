@@ -168,6 +168,39 @@ def test_store_placement_brute_force():
     assert (ks.reshape(nb * bs, -1)[~written] == 1).all()
 
 
+def test_store_torch_matches_store_oracle():
+    """The vectorized torch store (the bench's multi-core CPU baseline) writes
+    the same bytes and scales as the loop oracle: random rows over a wide
+    range of magnitudes, edge rows (zeros, -0, amax 448, tiny and huge),
+    skipped slots, and the reference-style int64 slot tensor."""
+    rng = np.random.default_rng(5)
+    nb, bs, h, d = 6, 32, 4, 128
+    n = 150
+    k = (rng.standard_normal((n, h, d)) * np.exp(rng.standard_normal((n, h, 1)) * 3)).astype(np.float32)
+    v = rng.standard_normal((n, h, d)).astype(np.float32)
+    k[0, 0] = 0.0
+    k[0, 1] = -0.0
+    k[1, 0] = np.linspace(-448, 448, d, dtype=np.float32)
+    k[1, 1] = rng.standard_normal(d).astype(np.float32) * 1e-39
+    v[2, 2] = rng.standard_normal(d).astype(np.float32) * 1e30
+    slots = rng.permutation(nb * bs)[:n]
+    slots[5] = -1
+    slots[6] = nb * bs
+    want = [np.zeros((nb, bs, h, d), np.uint8), np.zeros((nb, bs, h, d), np.uint8),
+            np.ones((nb, bs, h), np.float32), np.ones((nb, bs, h), np.float32)]
+    O.store_fp8_kvcache(k, v, *want, slots)
+    got = [torch.zeros(nb, bs, h, d, dtype=torch.uint8), torch.zeros(nb, bs, h, d, dtype=torch.uint8),
+           torch.ones(nb, bs, h), torch.ones(nb, bs, h)]
+    O.store_fp8_kvcache_torch(torch.from_numpy(k), torch.from_numpy(v), *got,
+                              torch.from_numpy(slots))
+    for g, w in zip(got, want):
+        g = g.numpy()
+        if g.dtype == np.float32:
+            assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
+        else:
+            assert np.array_equal(g, w)
+
+
 # ------------------------------------------------------------- attention ----
 
 def _filled_cache(rng, nb, bs, hk, d, tables, lens, scale_k=1.0, scale_v=1.0):
