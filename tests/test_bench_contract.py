@@ -45,3 +45,20 @@ def test_prefill_flops_count_every_visible_key():
     brute = 8 * 32 * visits * 4 * 128
     assert brute == 2_474_035_380_224
     assert bench.prefill_flops(8, 8192, 2048, 32, 128) == brute
+
+
+def test_committed_profiles_feed_the_bench_line():
+    """The roofline's traffic and each prefill object's MFMA fields are read
+    from the committed rocprofv3 summaries; every name bench.py asks for is
+    there, with a busy fraction in (0, 1]."""
+    traffic, src = bench.measured_traffic()
+    assert src == os.path.join("profiles", "decode_qwen3_8b_pmc.md")
+    alg = bench.decode_bytes(64, 4096, 32, 8, 128)
+    assert alg <= traffic < 1.1 * alg
+    for name in ("prefill_fp8_bf16", "prefill_fp8_fp16", "dense_prefill_bf16",
+                 "dense_prefill_fp16"):
+        c = bench.mfma_counters(name)
+        assert 0.0 < c["mfma_busy"] <= 1.0, name
+        assert c["valu_per_mfma"] > 1.0, name
+        res = bench._with_mfma({"frac": 0.25}, name)
+        assert res["frac_at_full_mfma"] >= 0.25
