@@ -89,6 +89,16 @@ __device__ __forceinline__ float rnd(float x) {
   return (float)(T)x;
 }
 
+// bf16: v_cvt_pk_bf16_f32 with x in the high half and zero in the low half
+// leaves a word that is the rounded value read as fp32, so the round trip
+// is one instruction (the plain cast converts and then shifts left by 16).
+// Same instruction, same rounding.
+template <>
+__device__ __forceinline__ float rnd<__bf16>(float x) {
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(float, __builtin_convertvector(f32x2{0.0f, x}, bf16x2));
+}
+
 // T(x) of a value that must first be rounded to fp32, as torch rounds x * r
 // before casting.  For fp16 the backend would otherwise fold the multiply
 // and the cast into one v_fma_mixlo_f16, which rounds once, and that differs
@@ -98,7 +108,7 @@ __device__ __forceinline__ float rnd(float x) {
 template <typename T>
 __device__ __forceinline__ float rnd_f32(float x) {
   asm volatile("" : "+v"(x));
-  return (float)(T)x;
+  return rnd<T>(x);
 }
 
 template <typename T>
