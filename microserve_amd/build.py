@@ -1,7 +1,8 @@
 """Build recipe for the mskv HIP library (gfx950 only).
 
 Compiles every source under ``csrc/`` with hipcc into
-``microserve_amd/libmskv.so``.  Run ``python -m microserve_amd.build``.
+``microserve_amd/libmskv.so``, and ``csrc/host/step_pack.cpp`` with g++
+into the ``microserve_amd._step_pack`` extension module.  Run ``python -m microserve_amd.build``.
 The library is built in-tree so it travels with the repository snapshot.
 """
 
@@ -11,11 +12,15 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libmskv.so")
 ARCH = "gfx950"
+# the host packer of the step-input builder, a CPython extension module
+PACK_SRC = os.path.join(CSRC, "host", "step_pack.cpp")
+PACK_OUT = os.path.join(HERE, "_step_pack" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 # -packed-fp32-ops: keep hipcc from emitting v_pk_{add,mul,fma}_f32.
 # No fast-math: the store path relies on hipcc's correctly rounded fp32
@@ -76,7 +81,23 @@ def build(verbose: bool = False) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp_out, OUT)
+    build_pack(verbose)
     return OUT
+
+
+def build_pack(verbose: bool = False) -> str:
+    """Compile the step-input packer (host C++, CPython API) with g++."""
+    cxx = shutil.which("g++") or "g++"
+    tmp_out = PACK_OUT + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall",
+           "-I" + sysconfig.get_paths()["include"], PACK_SRC, "-o", tmp_out]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"g++ failed on {PACK_SRC}:\n{r.stderr}")
+    os.replace(tmp_out, PACK_OUT)
+    return PACK_OUT
 
 
 if __name__ == "__main__":

@@ -12,8 +12,10 @@ with ``out`` it writes into the caller's fixed graph buffers.
 
 The reference writes every element with its own host-to-device copy.  Here
 the per-sequence state (scheduled token ids, first positions, token and table
-offsets, concatenated block tables) is packed with numpy into one pinned
-buffer, copied once, and ``mskv_build_step_inputs`` expands it on the GPU.
+offsets, concatenated block tables) is packed by the host extension
+``microserve_amd._step_pack`` (``csrc/host/step_pack.cpp``) in one pass over
+the sequences' lists, copied once through a pinned buffer, and
+``mskv_build_step_inputs`` expands it on the GPU.
 Sequences are duck-typed: anything with ``token_ids``,
 ``num_computed_tokens``, ``num_scheduled_tokens``, ``block_table`` and
 ``gap`` (``microserve/engine/sequence.py:19-50``).
@@ -21,13 +23,17 @@ Sequences are duck-typed: anything with ``token_ids``,
 
 from __future__ import annotations
 
-import itertools
-
 import numpy as np
 import torch
 
 from microserve_amd import _lib
 from microserve_amd.context import AttentionMode, Context
+
+try:
+    from microserve_amd import _step_pack
+except ImportError as e:  # pragma: no cover - raised on use, with the build command
+    raise ImportError("microserve_amd._step_pack is not built: run "
+                      "`python -m microserve_amd.build`") from e
 
 __all__ = ["compile_decode", "compile_prefill", "compile_chunk_prefill",
            "make_block_tables", "build_step_inputs"]
@@ -53,54 +59,20 @@ def build_step_inputs(seqs, block_size: int, device, *, pad_to: int | None = Non
     pad = nseq if pad_to is None else int(pad_to)
     if pad < nseq:
         raise ValueError(f"pad_to={pad} is smaller than the batch ({nseq})")
-    starts = np.fromiter((s.num_computed_tokens for s in seqs), np.int64, nseq)
-    ns = np.fromiter((s.num_scheduled_tokens for s in seqs), np.int64, nseq)
-    tlens = np.fromiter((len(s.block_table) for s in seqs), np.int64, nseq)
-    if nseq and (starts.min() < 0 or ns.min() < 0):
-        raise ValueError("negative num_computed_tokens or num_scheduled_tokens")
-    ends = starts + ns
-    sched = ns > 0
-    if np.any((ends[sched] - 1) // block_size >= tlens[sched]):
-        raise IndexError("list index out of range (block_table shorter than the "
-                         "scheduled positions)")
-    if any(e > len(s.token_ids) for e, s in zip(ends.tolist(), seqs)):
-        raise IndexError("list index out of range (token_ids shorter than the "
-                         "scheduled positions)")
-    total_q = int(ns.sum())
-    max_q = int(ns.max()) if nseq else 0
-    width = (int(tlens.max()) if nseq else 0) if table_width is None else int(table_width)
-    if width < (int(tlens.max()) if nseq else 0):
-        raise ValueError(f"table_width={width} is narrower than a block table")
-    if ends.size and ends.max() > np.iinfo(np.int32).max:
-        raise ValueError("positions beyond int32")
-    ntab = int(tlens.sum())
-    if dev.type == "cuda" and dev.index is None:
-        dev = torch.device("cuda", torch.cuda.current_device())
-
     # staging: int64 token ids, then int32 starts | cu_q | table offsets | tables
+    packed, total_q, max_q, _, max_tlen = _step_pack.pack(seqs, block_size)
+    width = max_tlen if table_width is None else int(table_width)
+    if width < max_tlen:
+        raise ValueError(f"table_width={width} is narrower than a block table")
     o_tok = 0
     o_start = 8 * total_q
     o_cu = o_start + 4 * nseq
     o_toff = o_cu + 4 * (nseq + 1)
     o_tab = o_toff + 4 * (nseq + 1)
-    nbytes = o_tab + 4 * ntab
-    host = torch.empty(max(nbytes, 8), dtype=torch.uint8, pin_memory=True)
-    hn = host.numpy()
-    if total_q:
-        hn[o_tok:o_start].view(np.int64)[:] = np.fromiter(
-            itertools.chain.from_iterable(
-                s.token_ids[st:st + n] for s, st, n in zip(seqs, starts.tolist(), ns.tolist())),
-            np.int64, total_q)
-    hn[o_start:o_cu].view(np.int32)[:] = starts
-    cu = hn[o_cu:o_toff].view(np.int32)
-    cu[0] = 0
-    cu[1:] = np.cumsum(ns)
-    toff = hn[o_toff:o_tab].view(np.int32)
-    toff[0] = 0
-    toff[1:] = np.cumsum(tlens)
-    if ntab:
-        hn[o_tab:nbytes].view(np.int32)[:] = np.fromiter(
-            itertools.chain.from_iterable(s.block_table for s in seqs), np.int32, ntab)
+    if dev.type == "cuda" and dev.index is None:
+        dev = torch.device("cuda", torch.cuda.current_device())
+    host = torch.empty(len(packed), dtype=torch.uint8, pin_memory=True)
+    host.numpy()[:] = np.frombuffer(packed, np.uint8)
     staged = torch.empty(host.numel(), dtype=torch.uint8, device=dev)
     staged.copy_(host, non_blocking=True)
 

@@ -78,3 +78,52 @@ def test_builder_raises_like_the_reference_on_short_tables():
         step_inputs.build_step_inputs([Seq(range(5), 4, 2, [0, 1])], 4, "cpu")
     with pytest.raises(AssertionError):
         step_inputs.compile_decode([Seq(range(9), 7, 1, [0, 1])], 4, "cpu")  # gap 2
+
+
+def _numpy_pack(seqs):
+    """The staging layout written out with numpy: int64 token ids of the
+    scheduled positions, then int32 first positions, cu_seqlens_q, table
+    offsets and the concatenated tables."""
+    ids = [t for s in seqs for t in s.token_ids[s.num_computed_tokens:
+                                                 s.num_computed_tokens + s.num_scheduled_tokens]]
+    ns = [s.num_scheduled_tokens for s in seqs]
+    tl = [len(s.block_table) for s in seqs]
+    parts = [np.asarray(ids, np.int64).tobytes(),
+             np.asarray([s.num_computed_tokens for s in seqs], np.int32).tobytes(),
+             np.concatenate([[0], np.cumsum(ns)]).astype(np.int32).tobytes(),
+             np.concatenate([[0], np.cumsum(tl)]).astype(np.int32).tobytes(),
+             np.asarray([b for s in seqs for b in s.block_table], np.int32).tobytes()]
+    raw = b"".join(parts)
+    return raw + bytes(max(0, 8 - len(raw)))
+
+
+@pytest.mark.parametrize("kind", ["decode", "prefill", "chunk"])
+def test_host_packer_layout(kind):
+    """The packer's bytes and sizes equal the layout written out with numpy,
+    on random batches, with tuple tables and an empty batch too."""
+    from microserve_amd import _step_pack
+    rng = np.random.default_rng(7)
+    for n_seqs in (0, 1, 5, 64):
+        seqs = random_batch(rng, kind, n_seqs, 16, 4096, 300)
+        if n_seqs > 1:
+            seqs[1].block_table = tuple(seqs[1].block_table)
+        raw, total_q, max_q, ntab, max_tlen = _step_pack.pack(seqs, 16)
+        assert raw == _numpy_pack(seqs), (kind, n_seqs)
+        assert total_q == sum(s.num_scheduled_tokens for s in seqs)
+        assert max_q == max((s.num_scheduled_tokens for s in seqs), default=0)
+        assert ntab == sum(len(s.block_table) for s in seqs)
+        assert max_tlen == max((len(s.block_table) for s in seqs), default=0)
+
+
+def test_host_packer_errors():
+    from microserve_amd import _step_pack
+    with pytest.raises(IndexError, match="block_table"):
+        _step_pack.pack([Seq(range(9), 8, 1, [0, 1])], 4)
+    with pytest.raises(IndexError, match="token_ids"):
+        _step_pack.pack([Seq(range(5), 4, 2, [0, 1])], 4)
+    with pytest.raises(ValueError, match="negative"):
+        _step_pack.pack([Seq(range(5), -1, 1, [0, 1])], 4)
+    with pytest.raises(OverflowError):
+        _step_pack.pack([Seq(range(5), 4, 1, [0, 1 << 40])], 4)
+    with pytest.raises(AttributeError):
+        _step_pack.pack([object()], 4)
