@@ -147,6 +147,11 @@ PyObject* pack(PyObject*, PyObject* args) {
     PyErr_SetString(PyExc_ValueError, "positions beyond int32");
     return nullptr;
   }
+  // cu_seqlens_q and the table offsets are int32 on the device
+  if (total_q > INT32_MAX || ntab > INT32_MAX) {
+    PyErr_SetString(PyExc_ValueError, "step too large for int32 offsets");
+    return nullptr;
+  }
   const long long o_start = 8 * total_q, o_cu = o_start + 4 * (long long)nseq;
   const long long o_toff = o_cu + 4 * ((long long)nseq + 1), o_tab = o_toff + 4 * ((long long)nseq + 1);
   const long long nbytes = o_tab + 4 * ntab;
