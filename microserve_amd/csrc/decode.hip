@@ -22,7 +22,9 @@
 //    of head n -- exactly the B-operand layout of O^T = V^T . P^T, so the
 //    probabilities never move between lanes.  P is scaled by the per-token
 //    v_scale and a per-wave power of two and rounded to fp16 for the PV
-//    MFMA (11 significant bits; the power of two keeps fp16's range).
+//    MFMA.  The power of two keeps fp16's range; a token whose v_scale lies
+//    within 2^21 of the largest the wave has seen keeps 11 significant
+//    bits, one further below gets a subnormal weight with fewer.
 //  * V^T's A operand needs eight tokens per lane at one d: it comes back
 //    out of the V tile transposed with ds_read_b64_tr_b8, then is converted
 //    fp8 -> fp16 (exact) in registers.
@@ -180,9 +182,10 @@ __device__ __forceinline__ void attend_range(const DecodeArgs& a, int b, int kvh
   l = 0.0f;
   // The PV operand is fp16(p * v_scale * f): f is a power of two with
   // v_scale * f <= kPvScaleMax for every valid token seen so far, so every
-  // weight stays within fp16's range (p < 2^8 under the lazy rescale) and
-  // fp16 keeps 11 significant bits; acc is in units of f, rescaled exactly
-  // when f shrinks.
+  // weight stays within fp16's range (p < 2^8 under the lazy rescale).  A
+  // weight keeps fp16's 11 significant bits while p * v_scale * f stays
+  // above fp16's smallest normal, 2^-14; acc is in units of f, rescaled
+  // exactly when f shrinks.
   float f = 0.0f, vseen = 0.0f;
 
   // ds_read_b64_tr_b8: in each 16-lane group, result byte e of lane i comes
